@@ -1,0 +1,114 @@
+/* whetstone_engine.h -- the batch=1 decode engine above the C ABI.
+ *
+ * A C++ restatement of the reference's caller side (crates/whetstone-core:
+ * Engine in engine.rs, ModelWeights in model.rs, the safe bindings of
+ * whetstone-kernels/src), which cannot be built here (no Rust toolchain). It
+ * drives libwhetstone_hip.so only through include/whetstone.h and
+ * include/whetstone_ext.h, and exposes a C API so Python (tests, bench.py) and
+ * any FFI can run the token loop.
+ *
+ * Two step implementations compute the same bits:
+ *   WSE_STEP_REFERENCE  the reference's launch sequence (engine.rs:512-572):
+ *                       rmsnorm, GEMV, rope_cache, attn (split+merge), GEMV,
+ *                       rmsnorm, GEMV, swiglu, GEMV per layer; ~11 launches/layer
+ *   WSE_STEP_FUSED      the MI355X sequence: RMSNorm folded into the GEMV
+ *                       prologue, RoPE/KV-append folded into attention, SwiGLU
+ *                       into the gate|up epilogue; 5 launches per layer.
+ */
+#ifndef WHETSTONE_ENGINE_H
+#define WHETSTONE_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "whetstone.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Model dimensions (crates/whetstone-core/src/config.rs:26-87, the subset the
+ * decode path reads). */
+typedef struct {
+  int32_t n_layers, hidden, n_q, n_kv, head_dim, inter, vocab;
+  int32_t tied;      /* lm_head is the embedding matrix */
+  int32_t qkv_bias;  /* q/k/v carry biases (Qwen2) */
+  int32_t qk_norm;   /* per-head q/k RMSNorm gains (Qwen3-style) */
+  int32_t rescore_k; /* > 0: keep an f16 head copy and rescore the top k */
+  float eps;
+  double rope_theta;
+} wse_config_t;
+
+typedef struct wse_model wse_model_t;
+/* Message of the last engine-level refusal on this thread (kernel-level
+ * failures report through wst_last_error). Never NULL. */
+const char *wse_last_error(void);
+typedef struct wse_engine wse_engine_t;
+
+enum { WSE_STEP_REFERENCE = 0, WSE_STEP_FUSED = 1 };
+
+/* Stage buckets of wse_engine_profile (engine/profile.rs:172-307). */
+enum {
+  WSE_STAGE_EMBED = 0,
+  WSE_STAGE_QKV = 1,     /* (rmsnorm +) qkv GEMV */
+  WSE_STAGE_ATTN = 2,    /* (rope +) attention */
+  WSE_STAGE_O = 3,
+  WSE_STAGE_GATE_UP = 4, /* (rmsnorm +) gate|up GEMV (+ swiglu) */
+  WSE_STAGE_DOWN = 5,
+  WSE_STAGE_HEAD = 6,    /* final norm + head GEMV */
+  WSE_STAGE_RESCORE = 7,
+  WSE_STAGE_SAMPLE = 8,  /* argmax + position advance */
+  WSE_STAGES = 9
+};
+
+/* Seeded synthetic weights generated and packed on the device: every Linear
+ * and the Embedding ~N(0,0.02) -> int4-hier-g32, q/k/v biases 0, norm gains 1,
+ * QK-norm gains 1+N(0,0.02), f16 head copy when rescore_k > 0. Same streams as
+ * the CPU oracle (oracle/oracle.c), so both hold identical bytes. */
+wst_status_t wse_model_synthetic(const wse_config_t *cfg, uint64_t seed, wse_model_t **out);
+void wse_model_free(wse_model_t *m);
+/* Device pointers of a packed matrix: "embed", "lm_head", "L<l>.qkv",
+ * "L<l>.o", "L<l>.gate_up", "L<l>.down". */
+wst_status_t wse_model_tensor(wse_model_t *m, const char *name, void **qw, void **si, void **sb,
+                              int64_t *in_f, int64_t *out_f);
+/* Weight bytes a decode step streams (packed matrices + norms + biases). */
+uint64_t wse_model_weight_bytes(const wse_model_t *m);
+
+wst_status_t wse_engine_create(wse_model_t *m, int32_t max_seq, int32_t step_mode,
+                               wse_engine_t **out);
+void wse_engine_free(wse_engine_t *e);
+wst_status_t wse_engine_reset(wse_engine_t *e);
+int32_t wse_engine_pos(const wse_engine_t *e);
+wst_status_t wse_engine_set_pos(wse_engine_t *e, int32_t pos);
+/* Synthetic context: KV caches of every layer filled for positions [0, n) with
+ * f16 N(0,1) from (seed, stream 1000+layer); position set to n. */
+wst_status_t wse_engine_fill_kv(wse_engine_t *e, uint64_t seed, int32_t n);
+/* Engine::forward (engine.rs:418-430): token -> device cursor, one step. */
+wst_status_t wse_engine_forward(wse_engine_t *e, int32_t token);
+/* Engine::step (engine.rs:480-499): one step on the token already in the
+ * device cursor (graph launch when captured). */
+wst_status_t wse_engine_step(wse_engine_t *e);
+/* Engine::capture_graph (engine.rs:357-393): warm-up step, rewind, capture. */
+wst_status_t wse_engine_capture_graph(wse_engine_t *e);
+/* Chunked prefill of n tokens (engine.rs:748-844), chunks of at most
+ * wst_chunk_max_tokens(); the last chunk computes the head for its last row
+ * and leaves the greedy pick in the token cursor. */
+wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids_host, int32_t n,
+                                 int32_t chunked);
+/* Greedy generation (engine.rs:909-956): prefill, then n_new tokens, each read
+ * back (4 bytes) from the device cursor. */
+wst_status_t wse_engine_generate(wse_engine_t *e, const int32_t *prompt_host, int32_t n_prompt,
+                                 int32_t n_new, int32_t chunked, int32_t *out_tokens_host);
+wst_status_t wse_engine_token(wse_engine_t *e, int32_t *out);
+wst_status_t wse_engine_logits(wse_engine_t *e, float *out_host);
+/* One eager step with an event at every stage boundary; adds the elapsed ms
+ * per stage into stage_ms[WSE_STAGES] and launch counts into counts. */
+wst_status_t wse_engine_profile_step(wse_engine_t *e, double *stage_ms, int32_t *counts);
+/* Algorithmic bytes of one decode step at the current position. */
+uint64_t wse_engine_step_bytes(const wse_engine_t *e);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WHETSTONE_ENGINE_H */

@@ -1,0 +1,99 @@
+/* whetstone_ext.h -- entry points of libwhetstone_hip.so that have NO
+ * counterpart in the reference's C ABI.
+ *
+ * Same conventions as whetstone.h (status codes, per-thread stream, device
+ * pointers). Two groups:
+ *
+ *  1. Fixture generation on the device. The reference quantises on the host in
+ *     Rust (crates/whetstone-quant/src/hier.rs); a 7B-shaped model is 7 G
+ *     weights, minutes of host time, so the synthetic configurations are
+ *     generated and packed on the GPU instead. The device packer follows
+ *     hier.rs:113-391 operation for operation and is checked bit-exact
+ *     against the host restatement.
+ *
+ *  2. Fused decode-step kernels used by the engine's fast path. Each computes
+ *     exactly what a sequence of reference ABI calls computes (named in its
+ *     comment), in fewer launches.
+ */
+#ifndef WHETSTONE_EXT_H
+#define WHETSTONE_EXT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "whetstone.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------ fixture generation */
+
+/* out[i] = fixture normal (seed, stream, index0 + i) * std as f32: the sum of
+ * twelve 16-bit uniforms drawn from splitmix64, re-centred, times 2^-16*std. */
+wst_status_t wst_fixture_normal_f32(void *out, size_t n, uint64_t seed, uint64_t stream,
+                                    uint64_t index0, float std_);
+/* Same values narrowed to f16, plus an f32 offset added before narrowing
+ * (norm gains are 1 + N(0, 0.02)). */
+wst_status_t wst_fixture_normal_f16(void *out, size_t n, uint64_t seed, uint64_t stream,
+                                    uint64_t index0, float std_, float offset);
+/* Generates rows [0, rows) of a tensor from (seed, stream) -- element (r, c) is
+ * fixture normal index r*in_f + c, times std -- and packs them to hier-g32 into
+ * rows [row0, row0+rows) of (qw, si, sb). Bit-exact with the host quantiser. */
+wst_status_t wst_fixture_pack_hier(void *qw, void *si, void *sb, int64_t in_f,
+                                   int64_t row0, int64_t rows, uint64_t seed,
+                                   uint64_t stream, float std_);
+/* Packs a caller-provided f32 matrix [rows][in_f] (device) into hier-g32. */
+wst_status_t wst_quantize_int4_hier(const void *w, void *qw, void *si, void *sb,
+                                    int64_t in_f, int64_t rows);
+/* Fills a KV cache [n_kv][max_seq][hd] f16 for positions [0, n): element
+ * (h, t, i) of k (kv=0) or v (kv=1) is f16(fixture normal (seed, stream,
+ * ((h*2+kv)<<20 + t)*hd + i)). */
+wst_status_t wst_fixture_fill_kv(void *k_cache, void *v_cache, int32_t n_kv,
+                                 int32_t max_seq, int32_t head_dim, int32_t n,
+                                 uint64_t seed, uint64_t stream);
+
+/* ------------------------------------------------ fused decode-step kernels */
+
+/* wst_rmsnorm(x, w, h) followed by wst_gemv_int4_hier_ex(W, h, bias, y, accum):
+ * every block recomputes the RMS of x (f32 [in_f]) and narrows x*inv*w to f16
+ * in registers, so the normalised vector never round-trips through memory.
+ * Also writes h (f16 [in_f]) from block 0 when h_out is non-NULL (the head
+ * rescore reads it). */
+wst_status_t wst_gemv_hier_rmsnorm(const void *qw, const void *si, const void *sb,
+                                   const void *x, const void *norm_w, float eps,
+                                   void *h_out, const void *bias, void *y, int32_t in_f,
+                                   int32_t out_f, int32_t accum);
+
+/* wst_gemv_int4_hier_ex over a fused gate|up matrix followed by wst_swiglu:
+ * row r of the gate half and row r of the up half are computed by the same
+ * lanes, and out[r] = f16(silu(g) * u) is written directly. Optional RMSNorm
+ * prologue when norm_w is non-NULL (as wst_gemv_hier_rmsnorm). */
+wst_status_t wst_gemv_hier_swiglu(const void *qw, const void *si, const void *sb,
+                                  const void *x, const void *norm_w, float eps,
+                                  void *out, int32_t in_f, int32_t inter);
+
+/* wst_rope_cache + wst_attn_decode in one launch. */
+wst_status_t wst_attn_decode_fused(void *qkv, void *k_cache, void *v_cache,
+                                   const void *cos_tab, const void *sin_tab, void *partials,
+                                   void *out, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                                   const void *pos, int32_t max_seq, float scale,
+                                   const void *q_norm_w, const void *k_norm_w, float eps);
+
+/* wst_argmax(logits, out_idx) followed by wst_advance_pos(pos, max_seq). */
+wst_status_t wst_argmax_advance(const void *logits, void *out_idx, int32_t n, void *pos,
+                                int32_t max_seq);
+
+/* wst_head_threshold + wst_head_compact + wst_head_rescore in two launches:
+ * the threshold ladder, then every logit >= threshold recomputed from the f16
+ * head by the block that found it. Rescores all selected rows whenever their
+ * count is <= cap (the reference's deterministic regime); above cap, none. */
+wst_status_t wst_head_rescore_fused(const void *head, const void *x, void *logits,
+                                    int32_t n, int32_t hidden, int32_t k, int32_t cap,
+                                    void *scratch, int32_t nblocks);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WHETSTONE_EXT_H */

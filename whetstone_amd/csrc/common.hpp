@@ -1,0 +1,267 @@
+// Internal helpers shared by the HIP sources. Not part of the C ABI.
+//
+// gfx950 (CDNA4) facts these helpers are written for: wave64, 256 compute
+// units in 8 XCDs, 160 KB LDS per CU, DPP lane permutes within 16-lane rows
+// plus row broadcasts across a wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "whetstone.h"
+#include "whetstone_ext.h"
+
+// ------------------------------------------------------- error propagation
+//
+// Per-thread message, as the reference keeps it (common.cuh:15-26,
+// runtime.cu:5-7): a failure is reported through the status code and
+// wst_last_error(), never by aborting.
+extern thread_local char wst_err_buf[512];
+
+inline void wst_set_error(const char *where, hipError_t e) {
+  snprintf(wst_err_buf, sizeof(wst_err_buf), "%s: %s (%s)", where, hipGetErrorString(e),
+           hipGetErrorName(e));
+}
+inline void wst_set_error_msg(const char *msg) {
+  snprintf(wst_err_buf, sizeof(wst_err_buf), "%s", msg);
+}
+
+#define WST_TRY(expr)                                                          \
+  do {                                                                         \
+    hipError_t _e = (expr);                                                    \
+    if (_e != hipSuccess) {                                                    \
+      wst_set_error(#expr, _e);                                                \
+      return WST_ERR_CUDA;                                                     \
+    }                                                                          \
+  } while (0)
+
+// Launch errors only; no device synchronisation (same contract as the
+// reference's WST_TRY_KERNEL, common.cuh:39-46).
+#define WST_TRY_KERNEL(name)                                                   \
+  do {                                                                         \
+    hipError_t _e = hipGetLastError();                                         \
+    if (_e != hipSuccess) {                                                    \
+      wst_set_error(name " (launch)", _e);                                     \
+      return WST_ERR_CUDA;                                                     \
+    }                                                                          \
+  } while (0)
+
+#define WST_REQUIRE(cond, msg)                                                 \
+  do {                                                                         \
+    if (!(cond)) {                                                             \
+      wst_set_error_msg(msg);                                                  \
+      return WST_ERR_INVALID_ARG;                                              \
+    }                                                                          \
+  } while (0)
+
+#define WST_STREAM hipStreamPerThread
+
+// --------------------------------------------------------- device facts
+
+// Compute units of the current device, cached per device ordinal: a property
+// query is far more expensive than the kernels it would size.
+int wst_cu_count();
+
+// A lazily created, zero-initialised device scratch region, one per (device,
+// slot). Created outside graph capture by the first eager call, exactly like
+// the reference's argmax scratch (sample.cu:82-88). Returns nullptr on failure
+// (message set).
+void *wst_static_scratch(int slot, size_t bytes);
+enum {
+  WST_SCRATCH_ARGMAX = 0,
+  WST_SCRATCH_ATTN = 1,
+  WST_SCRATCH_RESCORE = 2,
+  WST_SCRATCH_NLL = 3,
+  WST_SCRATCH_ENGINE = 4,
+  WST_SCRATCH_SLOTS = 8
+};
+
+// ----------------------------------------------------------- f16 helpers
+
+typedef _Float16 wst_h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float h2f(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+// f32 -> f16, round to nearest even. The empty asm pins `f` as an f32 value in
+// a VGPR: without it the compiler may fold the operation that produced `f`
+// into a mixed-precision op that rounds the exact result straight to f16
+// (v_fma_mix*), which differs from "round to f32, then to f16" at ties.
+__device__ __forceinline__ uint16_t f2h(float f) {
+  asm("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ wst_h2 as_h2(uint32_t u) { return __builtin_bit_cast(wst_h2, u); }
+
+// 16-byte streaming load with the non-temporal hint: data read exactly once
+// per call (packed weights) should not evict what is reused (activations).
+typedef uint32_t wst_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void *p) {
+  const wst_u32x4 v = __builtin_nontemporal_load((const wst_u32x4 *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ----------------------------------------------------------- reductions
+//
+// DPP sums. After dpp_sum16 every lane of each 16-lane row holds that row's
+// sum; quad_perm handles xor 1 and 2, half-mirror and mirror finish the row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float dpp_sum16(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  return v;
+}
+
+__device__ __forceinline__ float dpp_max16(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+// Sum over the 32 lanes of each half wave, returned in every lane of that half.
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v = dpp_sum16(v);
+  // Combine rows 0+1 and 2+3: every lane adds the value of lane ^ 16.
+  v += __shfl_xor(v, 16, 64);
+  return v;
+}
+
+// Sum over the whole wave, in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = dpp_sum16(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = dpp_max16(v);
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long t = __shfl_xor(v, o, 64);
+    v = t > v ? t : v;
+  }
+  return v;
+}
+
+// Block-wide sum for blocks of up to 1024 threads; every thread gets the
+// result. `red` holds 16 floats of LDS. Contains barriers.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nw = (blockDim.x + 63) >> 6;
+  v = wave_sum(v);
+  __syncthreads();  // `red` may still be read from a previous call
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.0f;
+  for (int i = 0; i < nw; ++i) s += red[i];  // fixed order: deterministic
+  return s;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nw = (blockDim.x + 63) >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = -INFINITY;
+  for (int i = 0; i < nw; ++i) s = fmaxf(s, red[i]);
+  return s;
+}
+
+// ------------------------------------------------------------- RMS scale
+//
+// 1/sqrt(mean(x^2) + eps) over n f32 values, for a 256-thread block: thread t
+// accumulates x[t], x[t+256], ... with fmaf, then block_sum. Every kernel that
+// normalises (the RMSNorm kernel and the GEMV prologues) calls this with 256
+// threads, so they all produce the same bits.
+__device__ __forceinline__ float rms_scale256(const float *__restrict__ x, int n, float eps,
+                                              float *red) {
+  float acc = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) acc = fmaf(x[i], x[i], acc);
+  acc = block_sum(acc, red);
+  return 1.0f / sqrtf(acc / (float)n + eps);
+}
+
+// ------------------------------------------------------------------ RoPE
+//
+// Half-rotation RoPE (decode.cu:112-178) with an explicit fma shape, so every
+// kernel that rotates (rope_cache, the fused attention prologue) rounds
+// identically.
+__device__ __forceinline__ float rope_lo(float x1, float x2, float c, float s) {
+  return fmaf(x1, c, -(x2 * s));
+}
+__device__ __forceinline__ float rope_hi(float x1, float x2, float c, float s) {
+  return fmaf(x2, c, x1 * s);
+}
+
+// Per-head QK-RMSNorm (common.cuh:185-202): thread j holds elements j and
+// j+half of the head; the block reduces over all hd elements; shared gain
+// [hd]. Called by every thread of the block (it contains barriers).
+__device__ __forceinline__ void qk_norm(float &x1, float &x2, const uint16_t *__restrict__ g,
+                                        int j, int half, int hd, float eps, bool active,
+                                        float *red) {
+  const float a = active ? fmaf(x1, x1, x2 * x2) : 0.0f;
+  const float ss = block_sum(a, red);
+  const float s = 1.0f / sqrtf(ss / (float)hd + eps);
+  if (active) {
+    x1 = x1 * s * h2f(g[j]);
+    x2 = x2 * s * h2f(g[j + half]);
+  }
+}
+
+// ------------------------------------------------------ argmax key
+//
+// Order-preserving key (sample.cu:28-37): value in the high word, complemented
+// index in the low word, so the u64 maximum is the largest value and, among
+// equal values, the lowest index.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)k << 32) | (unsigned long long)(~(uint32_t)idx);
+}
+
+// "Last block done": every block calls this once after publishing its partial
+// result with plain stores. The block that observes count == nblocks-1 returns
+// true (in every thread) and owns the final combine; it also resets the
+// counter to zero so the next launch (or a graph replay) starts clean. Device
+// scope release/acquire fences make the other blocks' stores visible across
+// XCDs.
+__device__ __forceinline__ bool last_block_done(unsigned int *counter, unsigned int nblocks) {
+  __shared__ bool is_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __atomic_thread_fence(__ATOMIC_RELEASE);
+    const unsigned int prev =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (prev == nblocks - 1);
+    if (is_last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (is_last) __atomic_thread_fence(__ATOMIC_ACQUIRE);
+  return is_last;
+}

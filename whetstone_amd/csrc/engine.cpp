@@ -1,0 +1,630 @@
+// The batch=1 decode engine: a C++ restatement of the reference's caller side
+// (crates/whetstone-core/src/engine.rs Engine, model.rs ModelWeights, and the
+// shape checks of crates/whetstone-kernels/src/*.rs). It talks to the GPU only
+// through the C ABI of libwhetstone_hip.so (include/whetstone.h,
+// include/whetstone_ext.h) -- the same boundary the reference's Rust engine
+// crosses -- and is compiled as plain host C++.
+#include "whetstone_engine.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "whetstone.h"
+#include "whetstone_ext.h"
+
+namespace {
+
+thread_local char g_msg[512];
+
+#define TRY(expr)                                  \
+  do {                                             \
+    const wst_status_t _s = (expr);                \
+    if (_s != WST_OK) return _s;                   \
+  } while (0)
+
+// Engine-level refusals carry their message in g_msg (wse_last_error); kernel
+// failures keep theirs in the library's wst_last_error.
+wst_status_t shape_error(const char *fmt, const char *what) {
+  snprintf(g_msg, sizeof(g_msg), fmt, what);
+  return WST_ERR_SHAPE;
+}
+
+struct Mat {
+  void *qw = nullptr, *si = nullptr, *sb = nullptr;
+  int64_t in_f = 0, out_f = 0;
+  uint64_t bytes() const { return (uint64_t)out_f * (uint64_t)(in_f / 2 + in_f / 32 + 4); }
+};
+
+struct Layer {
+  Mat qkv, o, gate_up, down;
+  void *qkv_bias = nullptr, *in_norm = nullptr, *post_norm = nullptr;
+  void *q_norm = nullptr, *k_norm = nullptr;
+};
+
+// Device allocations owned by a model or an engine, freed together.
+struct Arena {
+  std::vector<void *> ptrs;
+  wst_status_t alloc(void **out, size_t bytes, bool zero) {
+    *out = nullptr;
+    TRY(wst_malloc(out, bytes));
+    ptrs.push_back(*out);
+    if (zero) TRY(wst_memset(*out, 0, bytes));
+    return WST_OK;
+  }
+  void free_all() {
+    for (void *p : ptrs) wst_free(p);
+    ptrs.clear();
+  }
+};
+
+// Fixture streams, shared with the CPU oracle (oracle/oracle.c).
+enum { ST_Q = 0, ST_K = 1, ST_V = 2, ST_O = 3, ST_GATE = 4, ST_UP = 5, ST_DOWN = 6, ST_QN = 7, ST_KN = 8 };
+inline uint64_t stream_of(int l, int t) { return (uint64_t)l * 16u + (uint64_t)t + 16u; }
+constexpr uint64_t ST_EMBED = 1, ST_HEAD = 2;
+
+}  // namespace
+
+struct wse_model {
+  wse_config_t c{};
+  Mat embed, lm_head;
+  void *final_norm = nullptr;
+  void *rescore = nullptr;  // f16 [vocab][hidden]
+  std::vector<Layer> layers;
+  Arena arena;
+  const Mat &head() const { return c.tied ? embed : lm_head; }
+};
+
+struct wse_engine {
+  wse_model *m = nullptr;
+  int max_seq = 0, mode = WSE_STEP_FUSED, pos = 0;
+  void *x = nullptr, *h = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr,
+       *act = nullptr, *logits = nullptr, *token = nullptr, *pos_dev = nullptr;
+  std::vector<void *> kc, vc;
+  void *partials = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
+  // head rescore (rescore.rs:75-118)
+  int rs_k = 0, rs_cap = 0, rs_grid = 0, rs_nblocks = 0;
+  void *rs_thresh = nullptr, *rs_scratch = nullptr, *rs_count = nullptr, *rs_idx = nullptr;
+  void *graph = nullptr;
+  // chunk scratch, allocated on first use
+  int chunk_width = 0;
+  void *c_tokens = nullptr, *c_x = nullptr, *c_h = nullptr, *c_qkv = nullptr, *c_attn = nullptr,
+       *c_gu = nullptr, *c_act = nullptr;
+  std::vector<void *> events;
+  Arena arena;
+};
+
+extern "C" {
+
+const char *wse_last_error(void) { return g_msg; }
+
+// ------------------------------------------------------------------- model
+
+static wst_status_t alloc_mat(Arena &a, Mat &m, int64_t in_f, int64_t out_f) {
+  m.in_f = in_f;
+  m.out_f = out_f;
+  TRY(a.alloc(&m.qw, (size_t)(out_f * in_f / 2), false));
+  TRY(a.alloc(&m.si, (size_t)(out_f * in_f / 32), false));
+  TRY(a.alloc(&m.sb, (size_t)(out_f * 4), false));
+  return WST_OK;
+}
+
+static wst_status_t pack_part(Mat &m, int64_t row0, int64_t rows, uint64_t seed, uint64_t stream) {
+  return wst_fixture_pack_hier(m.qw, m.si, m.sb, m.in_f, row0, rows, seed, stream, 0.02f);
+}
+
+static wst_status_t f16_fill(Arena &a, void **out, size_t n, uint64_t seed, uint64_t stream,
+                             float std_, float offset) {
+  TRY(a.alloc(out, n * 2, false));
+  return wst_fixture_normal_f16(*out, n, seed, stream, 0, std_, offset);
+}
+
+static wst_status_t check_config(const wse_config_t *c) {
+  if (!c || c->n_layers <= 0 || c->hidden <= 0 || c->n_q <= 0 || c->n_kv <= 0 ||
+      c->head_dim <= 0 || c->inter <= 0 || c->vocab <= 0) {
+    snprintf(g_msg, sizeof(g_msg), "config: non-positive dimension");
+    return WST_ERR_SHAPE;
+  }
+  if (c->hidden % 32 || c->inter % 32 || (c->n_q * c->head_dim) % 32 || c->n_q % c->n_kv ||
+      c->head_dim % 2) {
+    snprintf(g_msg, sizeof(g_msg),
+             "config: hidden, intermediate and n_q*head_dim must be multiples of 32, n_q a "
+             "multiple of n_kv, head_dim even (config.rs:206-247)");
+    return WST_ERR_SHAPE;
+  }
+  return WST_OK;
+}
+
+static wst_status_t model_build(wse_model *m, uint64_t seed) {
+  const wse_config_t &c = m->c;
+  const int64_t H = c.hidden, hd = c.head_dim, I = c.inter, V = c.vocab;
+  const int64_t nq = (int64_t)c.n_q * hd, nk = (int64_t)c.n_kv * hd;
+  Arena &a = m->arena;
+  TRY(alloc_mat(a, m->embed, H, V));
+  TRY(pack_part(m->embed, 0, V, seed, ST_EMBED));
+  if (!c.tied) {
+    TRY(alloc_mat(a, m->lm_head, H, V));
+    TRY(pack_part(m->lm_head, 0, V, seed, ST_HEAD));
+  }
+  TRY(f16_fill(a, &m->final_norm, (size_t)H, seed, 0, 0.0f, 1.0f));
+  if (c.rescore_k > 0)
+    TRY(f16_fill(a, &m->rescore, (size_t)(V * H), seed, c.tied ? ST_EMBED : ST_HEAD, 0.02f, 0.0f));
+  m->layers.resize((size_t)c.n_layers);
+  for (int l = 0; l < c.n_layers; ++l) {
+    Layer &L = m->layers[(size_t)l];
+    TRY(alloc_mat(a, L.qkv, H, nq + 2 * nk));
+    TRY(pack_part(L.qkv, 0, nq, seed, stream_of(l, ST_Q)));
+    TRY(pack_part(L.qkv, nq, nk, seed, stream_of(l, ST_K)));
+    TRY(pack_part(L.qkv, nq + nk, nk, seed, stream_of(l, ST_V)));
+    TRY(alloc_mat(a, L.o, nq, H));
+    TRY(pack_part(L.o, 0, H, seed, stream_of(l, ST_O)));
+    TRY(alloc_mat(a, L.gate_up, H, 2 * I));
+    TRY(pack_part(L.gate_up, 0, I, seed, stream_of(l, ST_GATE)));
+    TRY(pack_part(L.gate_up, I, I, seed, stream_of(l, ST_UP)));
+    TRY(alloc_mat(a, L.down, I, H));
+    TRY(pack_part(L.down, 0, H, seed, stream_of(l, ST_DOWN)));
+    if (c.qkv_bias) TRY(a.alloc(&L.qkv_bias, (size_t)(nq + 2 * nk) * 2, true));
+    TRY(f16_fill(a, &L.in_norm, (size_t)H, seed, 0, 0.0f, 1.0f));
+    TRY(f16_fill(a, &L.post_norm, (size_t)H, seed, 0, 0.0f, 1.0f));
+    if (c.qk_norm) {
+      TRY(f16_fill(a, &L.q_norm, (size_t)hd, seed, stream_of(l, ST_QN), 0.02f, 1.0f));
+      TRY(f16_fill(a, &L.k_norm, (size_t)hd, seed, stream_of(l, ST_KN), 0.02f, 1.0f));
+    }
+  }
+  return wst_device_synchronize();
+}
+
+wst_status_t wse_model_synthetic(const wse_config_t *cfg, uint64_t seed, wse_model_t **out) {
+  if (!out) return WST_ERR_INVALID_ARG;
+  *out = nullptr;
+  TRY(check_config(cfg));
+  wse_model *m = new wse_model();
+  m->c = *cfg;
+  const wst_status_t st = model_build(m, seed);
+  if (st != WST_OK) {
+    wse_model_free(m);
+    return st;
+  }
+  *out = m;
+  return WST_OK;
+}
+
+void wse_model_free(wse_model_t *m) {
+  if (!m) return;
+  m->arena.free_all();
+  delete m;
+}
+
+wst_status_t wse_model_tensor(wse_model_t *m, const char *name, void **qw, void **si, void **sb,
+                              int64_t *in_f, int64_t *out_f) {
+  if (!m || !name || !qw || !si || !sb || !in_f || !out_f) return WST_ERR_INVALID_ARG;
+  const Mat *p = nullptr;
+  if (!strcmp(name, "embed")) p = &m->embed;
+  else if (!strcmp(name, "lm_head")) p = &m->head();
+  else {
+    int l = -1;
+    char what[32] = {0};
+    if (sscanf(name, "L%d.%31s", &l, what) == 2 && l >= 0 && l < m->c.n_layers) {
+      const Layer &L = m->layers[(size_t)l];
+      if (!strcmp(what, "qkv")) p = &L.qkv;
+      else if (!strcmp(what, "o")) p = &L.o;
+      else if (!strcmp(what, "gate_up")) p = &L.gate_up;
+      else if (!strcmp(what, "down")) p = &L.down;
+    }
+  }
+  if (!p) return shape_error("unknown tensor %s", name);
+  *qw = p->qw;
+  *si = p->si;
+  *sb = p->sb;
+  *in_f = p->in_f;
+  *out_f = p->out_f;
+  return WST_OK;
+}
+
+// config.rs:347-362 (decode_resident) restated for this layout: every packed
+// matrix the step streams, plus norm gains and biases. The embedding-row gather
+// and the rescore copy are excluded, as the reference excludes them.
+uint64_t wse_model_weight_bytes(const wse_model_t *m) {
+  if (!m) return 0;
+  const wse_config_t &c = m->c;
+  uint64_t b = m->head().bytes();
+  for (const Layer &L : m->layers) b += L.qkv.bytes() + L.o.bytes() + L.gate_up.bytes() + L.down.bytes();
+  b += (uint64_t)(2 * c.n_layers + 1) * (uint64_t)c.hidden * 2;
+  if (c.qkv_bias) b += (uint64_t)c.n_layers * (uint64_t)(c.n_q + 2 * c.n_kv) * c.head_dim * 2;
+  if (c.qk_norm) b += (uint64_t)c.n_layers * 2 * (uint64_t)c.head_dim * 2;
+  return b;
+}
+
+// ------------------------------------------------------------------ engine
+
+static wst_status_t rope_table(wse_engine *e) {
+  // decode.rs:95-147 (no scaling): invf = theta^(-j/half) in f64, angle p*invf
+  // in f64, narrowed to f32.
+  const int hd = e->m->c.head_dim, half = hd / 2;
+  std::vector<float> cs((size_t)e->max_seq * half), sn((size_t)e->max_seq * half);
+  for (int j = 0; j < half; ++j) {
+    const double invf = pow(e->m->c.rope_theta, -(double)j / (double)half);
+    for (int p = 0; p < e->max_seq; ++p) {
+      const double a = (double)p * invf;
+      cs[(size_t)p * half + j] = (float)cos(a);
+      sn[(size_t)p * half + j] = (float)sin(a);
+    }
+  }
+  TRY(e->arena.alloc(&e->cos_tab, cs.size() * 4, false));
+  TRY(e->arena.alloc(&e->sin_tab, sn.size() * 4, false));
+  TRY(wst_memcpy_h2d(e->cos_tab, cs.data(), cs.size() * 4));
+  TRY(wst_memcpy_h2d(e->sin_tab, sn.data(), sn.size() * 4));
+  return WST_OK;
+}
+
+static wst_status_t engine_build(wse_engine *e) {
+  const wse_config_t &c = e->m->c;
+  const size_t H = (size_t)c.hidden, hd = (size_t)c.head_dim, I = (size_t)c.inter,
+               V = (size_t)c.vocab;
+  const size_t nqkv = (size_t)(c.n_q + 2 * c.n_kv) * hd;
+  Arena &a = e->arena;
+  TRY(a.alloc(&e->x, H * 4, true));
+  TRY(a.alloc(&e->h, H * 2, true));
+  TRY(a.alloc(&e->qkv, nqkv * 4, true));
+  TRY(a.alloc(&e->attn, (size_t)c.n_q * hd * 2, true));
+  TRY(a.alloc(&e->gu, 2 * I * 4, true));
+  TRY(a.alloc(&e->act, I * 2, true));
+  TRY(a.alloc(&e->logits, V * 4, true));
+  TRY(a.alloc(&e->token, 4, true));
+  TRY(a.alloc(&e->pos_dev, 4, true));
+  const size_t kv = (size_t)c.n_kv * (size_t)e->max_seq * hd * 2;
+  e->kc.resize((size_t)c.n_layers);
+  e->vc.resize((size_t)c.n_layers);
+  for (int l = 0; l < c.n_layers; ++l) {
+    TRY(a.alloc(&e->kc[(size_t)l], kv, true));
+    TRY(a.alloc(&e->vc[(size_t)l], kv, true));
+  }
+  const int pf = wst_attn_partial_floats(c.n_q, c.head_dim, e->max_seq);
+  TRY(a.alloc(&e->partials, (size_t)(pf > 0 ? pf : 1) * 4, true));
+  TRY(rope_table(e));
+  if (c.rescore_k > 0 && e->m->rescore) {
+    // rescore.rs:90-118
+    e->rs_k = c.rescore_k;
+    e->rs_cap = c.rescore_k * 16 < c.vocab ? c.rescore_k * 16 : c.vocab;
+    if (e->rs_cap < e->rs_k) e->rs_cap = e->rs_k;
+    e->rs_grid = e->rs_cap < 256 ? e->rs_cap : 256;
+    int nb = (c.vocab + 255) / 256;
+    e->rs_nblocks = nb < 1 ? 1 : (nb > 512 ? 512 : nb);
+    TRY(a.alloc(&e->rs_thresh, 4, true));
+    TRY(a.alloc(&e->rs_scratch, (size_t)(e->rs_nblocks + 1 + 12) * 4, true));
+    TRY(a.alloc(&e->rs_count, 4, true));
+    TRY(a.alloc(&e->rs_idx, (size_t)e->rs_cap * 4, true));
+  }
+  return WST_OK;
+}
+
+wst_status_t wse_engine_create(wse_model_t *m, int32_t max_seq, int32_t step_mode,
+                               wse_engine_t **out) {
+  if (!m || !out || max_seq <= 0) return WST_ERR_INVALID_ARG;
+  *out = nullptr;
+  wse_engine *e = new wse_engine();
+  e->m = m;
+  e->max_seq = max_seq;
+  e->mode = step_mode == WSE_STEP_REFERENCE ? WSE_STEP_REFERENCE : WSE_STEP_FUSED;
+  if (e->mode == WSE_STEP_FUSED && m->c.head_dim > 128) e->mode = WSE_STEP_REFERENCE;
+  const wst_status_t st = engine_build(e);
+  if (st != WST_OK) {
+    wse_engine_free(e);
+    return st;
+  }
+  *out = e;
+  return WST_OK;
+}
+
+void wse_engine_free(wse_engine_t *e) {
+  if (!e) return;
+  if (e->graph) wst_graph_destroy(e->graph);
+  for (void *ev : e->events) wst_event_destroy(ev);
+  e->arena.free_all();
+  delete e;
+}
+
+int32_t wse_engine_pos(const wse_engine_t *e) { return e ? e->pos : -1; }
+
+wst_status_t wse_engine_set_pos(wse_engine_t *e, int32_t pos) {
+  if (!e || pos < 0 || pos > e->max_seq) return WST_ERR_INVALID_ARG;
+  e->pos = pos;
+  return wst_memcpy_h2d(e->pos_dev, &pos, 4);
+}
+
+wst_status_t wse_engine_reset(wse_engine_t *e) { return wse_engine_set_pos(e, 0); }
+
+wst_status_t wse_engine_fill_kv(wse_engine_t *e, uint64_t seed, int32_t n) {
+  if (!e || n < 0 || n > e->max_seq) return WST_ERR_INVALID_ARG;
+  const wse_config_t &c = e->m->c;
+  for (int l = 0; l < c.n_layers; ++l)
+    TRY(wst_fixture_fill_kv(e->kc[(size_t)l], e->vc[(size_t)l], c.n_kv, e->max_seq, c.head_dim, n,
+                            seed, 1000u + (uint64_t)l));
+  TRY(wst_device_synchronize());
+  return wse_engine_set_pos(e, n);
+}
+
+// ----------------------------------------------------------- the decode step
+
+struct Marks {
+  wse_engine *e;
+  bool on;
+  int next = 0;
+  std::vector<int> stage;  // stage of the interval ending at each mark
+  wst_status_t mark(int st) {
+    if (!on) return WST_OK;
+    if ((size_t)next >= e->events.size()) {
+      void *ev = nullptr;
+      TRY(wst_event_create(&ev));
+      e->events.push_back(ev);
+    }
+    stage.push_back(st);
+    return wst_event_record(e->events[(size_t)next++]);
+  }
+};
+
+// Engine::step_eager (engine.rs:512-572) in either launch sequence.
+static wst_status_t step_eager(wse_engine *e, Marks &mk) {
+  const wse_model &m = *e->m;
+  const wse_config_t &c = m.c;
+  const int H = c.hidden, hd = c.head_dim, nq = c.n_q, nkv = c.n_kv, I = c.inter, V = c.vocab;
+  const int nqkv = (nq + 2 * nkv) * hd;
+  const float eps = c.eps;
+  const float scale = (float)(1.0 / sqrt((double)hd));
+  const bool fused = e->mode == WSE_STEP_FUSED;
+  const Mat &head = m.head();
+
+  TRY(mk.mark(-1));
+  TRY(wst_embed_int4_hier(m.embed.qw, m.embed.si, m.embed.sb, e->token, e->x, H, V));
+  TRY(mk.mark(WSE_STAGE_EMBED));
+  for (int l = 0; l < c.n_layers; ++l) {
+    const Layer &L = m.layers[(size_t)l];
+    void *kc = e->kc[(size_t)l], *vc = e->vc[(size_t)l];
+    if (fused) {
+      TRY(wst_gemv_hier_rmsnorm(L.qkv.qw, L.qkv.si, L.qkv.sb, e->x, L.in_norm, eps, nullptr,
+                                L.qkv_bias, e->qkv, H, nqkv, 0));
+      TRY(mk.mark(WSE_STAGE_QKV));
+      TRY(wst_attn_decode_fused(e->qkv, kc, vc, e->cos_tab, e->sin_tab, e->partials, e->attn, nq,
+                                nkv, hd, e->pos_dev, e->max_seq, scale, L.q_norm, L.k_norm, eps));
+      TRY(mk.mark(WSE_STAGE_ATTN));
+      TRY(wst_gemv_int4_hier_ex(L.o.qw, L.o.si, L.o.sb, e->attn, nullptr, e->x, nq * hd, H, 1));
+      TRY(mk.mark(WSE_STAGE_O));
+      TRY(wst_gemv_hier_swiglu(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->x, L.post_norm, eps,
+                               e->act, H, I));
+      TRY(mk.mark(WSE_STAGE_GATE_UP));
+    } else {
+      TRY(wst_rmsnorm(e->x, L.in_norm, e->h, H, eps));
+      TRY(wst_gemv_int4_hier_ex(L.qkv.qw, L.qkv.si, L.qkv.sb, e->h, L.qkv_bias, e->qkv, H, nqkv, 0));
+      TRY(mk.mark(WSE_STAGE_QKV));
+      TRY(wst_rope_cache(e->qkv, kc, vc, e->cos_tab, e->sin_tab, nq, nkv, hd, e->pos_dev,
+                         e->max_seq, L.q_norm, L.k_norm, eps));
+      TRY(wst_attn_decode(e->qkv, kc, vc, e->partials, e->attn, nq, nkv, hd, e->pos_dev,
+                          e->max_seq, scale));
+      TRY(mk.mark(WSE_STAGE_ATTN));
+      TRY(wst_gemv_int4_hier_ex(L.o.qw, L.o.si, L.o.sb, e->attn, nullptr, e->x, nq * hd, H, 1));
+      TRY(mk.mark(WSE_STAGE_O));
+      TRY(wst_rmsnorm(e->x, L.post_norm, e->h, H, eps));
+      TRY(wst_gemv_int4_hier_ex(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->h, nullptr, e->gu, H,
+                                2 * I, 0));
+      TRY(wst_swiglu(e->gu, e->act, I));
+      TRY(mk.mark(WSE_STAGE_GATE_UP));
+    }
+    TRY(wst_gemv_int4_hier_ex(L.down.qw, L.down.si, L.down.sb, e->act, nullptr, e->x, I, H, 1));
+    TRY(mk.mark(WSE_STAGE_DOWN));
+  }
+  if (fused) {
+    TRY(wst_gemv_hier_rmsnorm(head.qw, head.si, head.sb, e->x, m.final_norm, eps, e->h, nullptr,
+                              e->logits, H, V, 0));
+  } else {
+    TRY(wst_rmsnorm(e->x, m.final_norm, e->h, H, eps));
+    TRY(wst_gemv_int4_hier_ex(head.qw, head.si, head.sb, e->h, nullptr, e->logits, H, V, 0));
+  }
+  TRY(mk.mark(WSE_STAGE_HEAD));
+  if (e->rs_k > 0) {
+    if (fused) {
+      TRY(wst_head_rescore_fused(m.rescore, e->h, e->logits, V, H, e->rs_k, e->rs_cap,
+                                 e->rs_scratch, e->rs_nblocks));
+    } else {
+      TRY(wst_head_threshold(e->logits, V, e->rs_k, e->rs_cap, e->rs_scratch, e->rs_nblocks,
+                             e->rs_thresh, e->rs_count));
+      TRY(wst_head_compact(e->logits, V, e->rs_thresh, e->rs_count, e->rs_idx, e->rs_cap));
+      TRY(wst_head_rescore(m.rescore, e->h, e->rs_idx, e->rs_count, e->logits, H, e->rs_cap,
+                           e->rs_grid));
+    }
+    TRY(mk.mark(WSE_STAGE_RESCORE));
+  }
+  if (fused) {
+    TRY(wst_argmax_advance(e->logits, e->token, V, e->pos_dev, e->max_seq));
+  } else {
+    TRY(wst_argmax(e->logits, e->token, V));
+    TRY(wst_advance_pos(e->pos_dev, e->max_seq));
+  }
+  TRY(mk.mark(WSE_STAGE_SAMPLE));
+  return WST_OK;
+}
+
+static wst_status_t check_room(wse_engine *e) {
+  if (e->pos >= e->max_seq) {
+    snprintf(g_msg, sizeof(g_msg), "context is full at %d tokens", e->max_seq);
+    return WST_ERR_SHAPE;
+  }
+  return WST_OK;
+}
+
+wst_status_t wse_engine_step(wse_engine_t *e) {
+  if (!e) return WST_ERR_INVALID_ARG;
+  TRY(check_room(e));
+  if (e->graph) {
+    TRY(wst_graph_launch(e->graph));
+  } else {
+    Marks mk{e, false};
+    TRY(step_eager(e, mk));
+  }
+  e->pos += 1;
+  return WST_OK;
+}
+
+wst_status_t wse_engine_forward(wse_engine_t *e, int32_t token) {
+  if (!e) return WST_ERR_INVALID_ARG;
+  TRY(check_room(e));
+  TRY(wst_memcpy_h2d(e->token, &token, 4));
+  return wse_engine_step(e);
+}
+
+wst_status_t wse_engine_capture_graph(wse_engine_t *e) {
+  if (!e) return WST_ERR_INVALID_ARG;
+  if (e->graph) return WST_OK;
+  // Warm every lazily initialised path (static scratch, cached device facts)
+  // outside the capture, then rewind (engine.rs:357-393).
+  const int saved = e->pos;
+  int32_t tok = 0;
+  TRY(wst_memcpy_d2h(&tok, e->token, 4));
+  {
+    Marks mk{e, false};
+    TRY(step_eager(e, mk));
+  }
+  TRY(wst_device_synchronize());
+  TRY(wse_engine_set_pos(e, saved));
+  TRY(wst_memcpy_h2d(e->token, &tok, 4));
+  TRY(wst_graph_capture_begin());
+  Marks mk{e, false};
+  const wst_status_t st = step_eager(e, mk);
+  void *exec = nullptr;
+  const wst_status_t st2 = wst_graph_capture_end(&exec);  // always end the capture
+  TRY(st);
+  TRY(st2);
+  e->graph = exec;
+  return WST_OK;
+}
+
+wst_status_t wse_engine_profile_step(wse_engine_t *e, double *stage_ms, int32_t *counts) {
+  if (!e || !stage_ms) return WST_ERR_INVALID_ARG;
+  TRY(check_room(e));
+  Marks mk{e, true};
+  TRY(step_eager(e, mk));
+  e->pos += 1;
+  for (int i = 1; i < mk.next; ++i) {
+    float ms = 0.0f;
+    TRY(wst_event_elapsed_ms(e->events[(size_t)i - 1], e->events[(size_t)i], &ms));
+    const int st = mk.stage[(size_t)i];
+    if (st >= 0 && st < WSE_STAGES) {
+      stage_ms[st] += ms;
+      if (counts) counts[st] += 1;
+    }
+  }
+  return WST_OK;
+}
+
+wst_status_t wse_engine_token(wse_engine_t *e, int32_t *out) {
+  if (!e || !out) return WST_ERR_INVALID_ARG;
+  return wst_memcpy_d2h(out, e->token, 4);
+}
+
+wst_status_t wse_engine_logits(wse_engine_t *e, float *out) {
+  if (!e || !out) return WST_ERR_INVALID_ARG;
+  return wst_memcpy_d2h(out, e->logits, (size_t)e->m->c.vocab * 4);
+}
+
+uint64_t wse_engine_step_bytes(const wse_engine_t *e) {
+  if (!e) return 0;
+  const wse_config_t &c = e->m->c;
+  const uint64_t seq = (uint64_t)(e->pos + 1 < e->max_seq ? e->pos + 1 : e->max_seq);
+  const uint64_t kv = (uint64_t)c.n_layers * 2 * (uint64_t)c.n_kv * (uint64_t)c.head_dim * 2 * seq;
+  return wse_model_weight_bytes(e->m) + kv;
+}
+
+// ---------------------------------------------------------------- prefill
+
+static wst_status_t ensure_chunk(wse_engine *e) {
+  if (e->chunk_width) return WST_OK;
+  const wse_config_t &c = e->m->c;
+  const size_t w = (size_t)wst_chunk_max_tokens();
+  const size_t H = (size_t)c.hidden, hd = (size_t)c.head_dim, I = (size_t)c.inter;
+  const size_t nqkv = (size_t)(c.n_q + 2 * c.n_kv) * hd;
+  Arena &a = e->arena;
+  TRY(a.alloc(&e->c_tokens, w * 4, true));
+  TRY(a.alloc(&e->c_x, w * H * 4, true));
+  TRY(a.alloc(&e->c_h, w * H * 2, true));
+  TRY(a.alloc(&e->c_qkv, w * nqkv * 4, true));
+  TRY(a.alloc(&e->c_attn, w * (size_t)c.n_q * hd * 2, true));
+  TRY(a.alloc(&e->c_gu, w * 2 * I * 4, true));
+  TRY(a.alloc(&e->c_act, w * I * 2, true));
+  e->chunk_width = (int)w;
+  return WST_OK;
+}
+
+// Engine::forward_chunk_ex (engine.rs:748-844). The head runs only for the
+// chunk's last row, on the single-token buffers, when want_logits.
+static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool want_logits) {
+  const wse_model &m = *e->m;
+  const wse_config_t &c = m.c;
+  const int H = c.hidden, hd = c.head_dim, nq = c.n_q, nkv = c.n_kv, I = c.inter, V = c.vocab;
+  const int nqkv = (nq + 2 * nkv) * hd;
+  const float eps = c.eps, scale = (float)(1.0 / sqrt((double)hd));
+  if (e->pos + n > e->max_seq) {
+    snprintf(g_msg, sizeof(g_msg), "prefill: %d tokens at position %d exceed the %d token cache",
+             n, e->pos, e->max_seq);
+    return WST_ERR_SHAPE;
+  }
+  const int pos0 = e->pos;
+  TRY(wst_memcpy_h2d(e->c_tokens, ids, (size_t)n * 4));
+  TRY(wst_embed_int4_hier_chunk(m.embed.qw, m.embed.si, m.embed.sb, e->c_tokens, e->c_x, H, V, n));
+  for (int l = 0; l < c.n_layers; ++l) {
+    const Layer &L = m.layers[(size_t)l];
+    TRY(wst_rmsnorm_chunk(e->c_x, L.in_norm, e->c_h, H, n, eps));
+    TRY(wst_gemm_int4_hier(L.qkv.qw, L.qkv.si, L.qkv.sb, e->c_h, L.qkv_bias, e->c_qkv, H, nqkv, n, 0));
+    TRY(wst_rope_cache_chunk(e->c_qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab, e->sin_tab,
+                             nq, nkv, hd, pos0, n, e->max_seq, L.q_norm, L.k_norm, eps));
+    TRY(wst_attn_chunk(e->c_qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->c_attn, nq, nkv, hd, pos0,
+                       n, e->max_seq, scale));
+    TRY(wst_gemm_int4_hier(L.o.qw, L.o.si, L.o.sb, e->c_attn, nullptr, e->c_x, nq * hd, H, n, 1));
+    TRY(wst_rmsnorm_chunk(e->c_x, L.post_norm, e->c_h, H, n, eps));
+    TRY(wst_gemm_int4_hier(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->c_h, nullptr, e->c_gu, H,
+                           2 * I, n, 0));
+    TRY(wst_swiglu_chunk(e->c_gu, e->c_act, I, n));
+    TRY(wst_gemm_int4_hier(L.down.qw, L.down.si, L.down.sb, e->c_act, nullptr, e->c_x, I, H, n, 1));
+  }
+  if (want_logits) {
+    const Mat &head = m.head();
+    void *last = (char *)e->c_x + (size_t)(n - 1) * H * 4;
+    TRY(wst_rmsnorm(last, m.final_norm, e->h, H, eps));
+    TRY(wst_gemv_int4_hier_ex(head.qw, head.si, head.sb, e->h, nullptr, e->logits, H, V, 0));
+    TRY(wst_argmax(e->logits, e->token, V));
+  }
+  return wse_engine_set_pos(e, pos0 + n);
+}
+
+wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids, int32_t n, int32_t chunked) {
+  if (!e || !ids || n <= 0) return WST_ERR_INVALID_ARG;
+  if (chunked && n > 1) {
+    TRY(ensure_chunk(e));
+    const int w = e->chunk_width;
+    for (int s = 0; s < n; s += w) {
+      const int k = n - s < w ? n - s : w;
+      TRY(forward_chunk(e, ids + s, k, s + k == n));
+    }
+    return WST_OK;
+  }
+  for (int i = 0; i < n; ++i) TRY(wse_engine_forward(e, ids[i]));
+  return WST_OK;
+}
+
+wst_status_t wse_engine_generate(wse_engine_t *e, const int32_t *prompt, int32_t n_prompt,
+                                 int32_t n_new, int32_t chunked, int32_t *out) {
+  if (!e || !prompt || n_prompt <= 0 || n_new < 0 || (n_new && !out)) return WST_ERR_INVALID_ARG;
+  TRY(wse_engine_prefill(e, prompt, n_prompt, chunked));
+  int32_t next = 0;
+  TRY(wse_engine_token(e, &next));
+  for (int i = 0; i < n_new; ++i) {
+    out[i] = next;
+    if (i + 1 == n_new || e->pos >= e->max_seq) break;
+    TRY(wse_engine_step(e));
+    TRY(wse_engine_token(e, &next));
+  }
+  return WST_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,207 @@
+"""Python handle on the C++ decode engine (include/whetstone_engine.h).
+
+The engine restates the reference's Engine (crates/whetstone-core/src/engine.rs)
+over the C ABI; this module only binds it. There is no Python or CPU fallback:
+a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import ffi
+
+STEP_REFERENCE = 0
+STEP_FUSED = 1
+STAGES = ["embed", "qkv", "attn", "o", "gate_up", "down", "head", "rescore", "sample"]
+
+
+class Config(C.Structure):
+    """wse_config_t; field order matches oracle.Config."""
+    _fields_ = [
+        ("n_layers", C.c_int32), ("hidden", C.c_int32), ("n_q", C.c_int32),
+        ("n_kv", C.c_int32), ("head_dim", C.c_int32), ("inter", C.c_int32),
+        ("vocab", C.c_int32), ("tied", C.c_int32), ("qkv_bias", C.c_int32),
+        ("qk_norm", C.c_int32), ("rescore_k", C.c_int32), ("eps", C.c_float),
+        ("rope_theta", C.c_double),
+    ]
+
+
+# Shapes of BASELINE.json's configurations (config.rs conventions).
+QWEN05B = dict(n_layers=24, hidden=896, n_q=14, n_kv=2, head_dim=64, inter=4864,
+               vocab=151936, tied=1, qkv_bias=1, qk_norm=0, rescore_k=0, eps=1e-6,
+               rope_theta=1e6)
+QWEN7B = dict(n_layers=28, hidden=3584, n_q=28, n_kv=4, head_dim=128, inter=18944,
+              vocab=152064, tied=0, qkv_bias=1, qk_norm=0, rescore_k=0, eps=1e-6,
+              rope_theta=1e6)
+
+P = C.c_void_p
+PP = C.POINTER(C.c_void_p)
+I32 = C.c_int32
+_SIG = {
+    "wse_last_error": (C.c_char_p, []),
+    "wse_model_synthetic": (I32, [C.POINTER(Config), C.c_uint64, PP]),
+    "wse_model_free": (None, [P]),
+    "wse_model_tensor": (I32, [P, C.c_char_p, PP, PP, PP, C.POINTER(C.c_int64),
+                               C.POINTER(C.c_int64)]),
+    "wse_model_weight_bytes": (C.c_uint64, [P]),
+    "wse_engine_create": (I32, [P, I32, I32, PP]),
+    "wse_engine_free": (None, [P]),
+    "wse_engine_reset": (I32, [P]),
+    "wse_engine_pos": (I32, [P]),
+    "wse_engine_set_pos": (I32, [P, I32]),
+    "wse_engine_fill_kv": (I32, [P, C.c_uint64, I32]),
+    "wse_engine_forward": (I32, [P, I32]),
+    "wse_engine_step": (I32, [P]),
+    "wse_engine_capture_graph": (I32, [P]),
+    "wse_engine_prefill": (I32, [P, P, I32, I32]),
+    "wse_engine_generate": (I32, [P, P, I32, I32, I32, P]),
+    "wse_engine_token": (I32, [P, C.POINTER(I32)]),
+    "wse_engine_logits": (I32, [P, P]),
+    "wse_engine_profile_step": (I32, [P, C.POINTER(C.c_double), C.POINTER(I32)]),
+    "wse_engine_step_bytes": (C.c_uint64, [P]),
+}
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        ffi.lib()  # the kernel library first (the engine links against it)
+        if not ffi.ENGINE_LIB.exists():
+            raise FileNotFoundError(f"{ffi.ENGINE_LIB} is missing; run python -m whetstone_amd.build")
+        L = C.CDLL(str(ffi.ENGINE_LIB))
+        for name, (res, args) in _SIG.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(st: int) -> None:
+    if st != ffi.WST_OK:
+        msg = lib().wse_last_error().decode(errors="replace")
+        kmsg = ffi.lib().wst_last_error().decode(errors="replace")
+        raise ffi.WstError(st, f"{msg} | {kmsg}")
+
+
+class Model:
+    """Seeded synthetic weights, generated and packed in HBM."""
+
+    def __init__(self, cfg: dict, seed: int = 0):
+        self.cfg = dict(cfg)
+        self._c = Config(**self.cfg)
+        h = C.c_void_p()
+        _check(lib().wse_model_synthetic(C.byref(self._c), seed, C.byref(h)))
+        self.h = h
+
+    def tensor(self, name: str):
+        qw, si, sb = C.c_void_p(), C.c_void_p(), C.c_void_p()
+        i, o = C.c_int64(), C.c_int64()
+        _check(lib().wse_model_tensor(self.h, name.encode(), C.byref(qw), C.byref(si),
+                                      C.byref(sb), C.byref(i), C.byref(o)))
+        return qw.value, si.value, sb.value, i.value, o.value
+
+    def tensor_host(self, name: str, rows=None):
+        """Copies (a row range of) a packed matrix to the host."""
+        qw, si, sb, i, o = self.tensor(name)
+        r0, r1 = (0, o) if rows is None else rows
+        n = r1 - r0
+        q = np.empty(n * i // 8, np.uint32)
+        s = np.empty(n * i // 32, np.uint8)
+        b = np.empty(n, np.uint32)
+        ffi.check(ffi.lib().wst_memcpy_d2h(q.ctypes.data, qw + r0 * i // 2, q.nbytes))
+        ffi.check(ffi.lib().wst_memcpy_d2h(s.ctypes.data, si + r0 * i // 32, s.nbytes))
+        ffi.check(ffi.lib().wst_memcpy_d2h(b.ctypes.data, sb + r0 * 4, b.nbytes))
+        return q, s, b, i, n
+
+    def weight_bytes(self) -> int:
+        return int(lib().wse_model_weight_bytes(self.h))
+
+    def close(self):
+        if self.h is not None and self.h.value:
+            lib().wse_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Engine:
+    def __init__(self, model: Model, max_seq: int, mode: int = STEP_FUSED):
+        self.model = model
+        h = C.c_void_p()
+        _check(lib().wse_engine_create(model.h, max_seq, mode, C.byref(h)))
+        self.h = h
+        self.max_seq = max_seq
+        self.vocab = model.cfg["vocab"]
+
+    @property
+    def pos(self) -> int:
+        return int(lib().wse_engine_pos(self.h))
+
+    def set_pos(self, p: int):
+        _check(lib().wse_engine_set_pos(self.h, p))
+
+    def reset(self):
+        _check(lib().wse_engine_reset(self.h))
+
+    def fill_kv(self, seed: int, n: int):
+        _check(lib().wse_engine_fill_kv(self.h, seed, n))
+
+    def forward(self, token: int):
+        _check(lib().wse_engine_forward(self.h, token))
+
+    def step(self):
+        _check(lib().wse_engine_step(self.h))
+
+    def capture_graph(self):
+        _check(lib().wse_engine_capture_graph(self.h))
+
+    def prefill(self, ids, chunked: bool = True):
+        a = np.ascontiguousarray(ids, np.int32)
+        _check(lib().wse_engine_prefill(self.h, a.ctypes.data, a.size, int(chunked)))
+
+    def generate(self, prompt, n_new: int, chunked: bool = True) -> np.ndarray:
+        a = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(n_new, 1), np.int32)
+        _check(lib().wse_engine_generate(self.h, a.ctypes.data, a.size, n_new, int(chunked),
+                                         out.ctypes.data))
+        return out[:n_new]
+
+    def token(self) -> int:
+        t = C.c_int32()
+        _check(lib().wse_engine_token(self.h, C.byref(t)))
+        return t.value
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        _check(lib().wse_engine_logits(self.h, out.ctypes.data))
+        return out
+
+    def profile_step(self, acc=None, counts=None):
+        acc = np.zeros(len(STAGES), np.float64) if acc is None else acc
+        counts = np.zeros(len(STAGES), np.int32) if counts is None else counts
+        _check(lib().wse_engine_profile_step(
+            self.h, acc.ctypes.data_as(C.POINTER(C.c_double)),
+            counts.ctypes.data_as(C.POINTER(C.c_int32))))
+        return acc, counts
+
+    def step_bytes(self) -> int:
+        return int(lib().wse_engine_step_bytes(self.h))
+
+    def close(self):
+        if self.h is not None and self.h.value:
+            lib().wse_engine_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
