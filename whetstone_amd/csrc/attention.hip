@@ -4,38 +4,51 @@
 //
 // MI355X design
 // -------------
-// * One block per (kv head, sequence slice) rather than per (query head,
-//   slice): every K/V element is read from memory once and used for all
-//   n_q/n_kv query heads of the group, instead of relying on L2 hits that a
-//   per-XCD L2 does not guarantee across blocks.
+// * One 512-thread block per (kv head, sequence slice) rather than per
+//   (query head, slice): every K/V element is read from memory once and used
+//   for all n_q/n_kv query heads of the group, instead of relying on L2 hits
+//   that a per-XCD L2 does not guarantee across blocks.
 // * A position's head vector is split over hd/8 lanes, 16 B (8 halves) per
-//   lane per load, so one wave reads 64/(hd/8) positions of K and V per step
-//   with dwordx4 loads.
+//   lane per load. Each wave sweeps ATTN_UNROLL steps of 64/(hd/8) positions
+//   per iteration and issues all of an iteration's K/V loads before it uses
+//   any; at the configurations' contexts a slice is one iteration, so the
+//   whole slice is requested in one round trip.
 // * Scores reduce across the hd/8 lanes of a position; each position-group of
 //   lanes keeps its own online-softmax state per query head, merged across
-//   groups by lane shuffles and across the 4 waves through LDS.
+//   groups by lane shuffles and across the 8 waves through LDS.
 // * The slice merge is done by the last block of each kv head to finish (a
 //   device-scope counter that the merging block resets), so the whole
 //   attention is one launch and the counter needs no memset inside a graph.
-//   Slices and waves are merged in a fixed order: results are deterministic.
-// * ROPE form (wst_attn_decode_fused): each block first applies QK-norm and
-//   RoPE to the q heads it needs, exactly as wst_rope_cache does (same
-//   per-head reduction, same fma shapes), keeps them in LDS, and the block
-//   whose slice holds the current position appends that position's k and v to
-//   the cache before reading it. No other block reads that position, so no
-//   cross-block wait is needed, and the result is bit-identical to
-//   wst_rope_cache followed by wst_attn_decode.
+//   The merging threads fetch every slice's partial in one batch of loads.
+//   Slices and waves merge in a fixed order: results are deterministic.
+// * ROPE form (wst_attn_decode_fused): each block applies QK-norm and RoPE to
+//   the q heads it needs exactly as wst_rope_cache does (same per-head
+//   reduction, same fma shapes) while its first K/V loads are in flight; the
+//   block whose slice holds the current position appends that position's k
+//   and v to the cache and uses them from LDS. No other block reads that
+//   position, so no cross-block wait is needed, and the result is bit-identical
+//   to wst_rope_cache followed by wst_attn_decode.
 #include "common.hpp"
 
+#include <stdlib.h>
+
 #define ATTN_MAX_GQA 8
-#define ATTN_MAX_SPLITS 64
+#define ATTN_MAX_SPLITS 16
 #define ATTN_UNROLL 4
+#define ATTN_WAVES 8
+#define ATTN_THREADS (64 * ATTN_WAVES)
 
 static inline int attn_splits(int n_kv, int max_seq) {
-  // ~2 blocks per CU, but never slices thinner than 128 cached positions: a
-  // slice is one or two unrolled sweeps of a block, and the merge reads every
-  // slice's partial.
-  int s = (2 * wst_cu_count() + n_kv - 1) / n_kv;
+  // Slices of at least 128 cached positions, at most 16 of them (the merge
+  // fetches every slice in one batch), and no more than ~1 block per CU.
+  // WST_ATTN_SPLITS caps the slice count (for sweeps).
+  static int cap_env = -1;
+  if (cap_env < 0) {
+    const char *e = getenv("WST_ATTN_SPLITS");
+    cap_env = e ? atoi(e) : 0;
+  }
+  int s = (wst_cu_count() + n_kv - 1) / n_kv;
+  if (cap_env > 0 && s > cap_env) s = cap_env;
   const int by_len = (max_seq + 127) / 128;
   if (s > by_len) s = by_len;
   if (s > ATTN_MAX_SPLITS) s = ATTN_MAX_SPLITS;
@@ -61,14 +74,39 @@ struct RopeArgs {
   float eps;
 };
 
+// Sum over the LP lanes of a position (aligned groups of 8, 16 or 32 lanes),
+// returned in all of them. DPP row operations (quad swaps, half-row and row
+// mirrors): a few VALU cycles per step, where lane shuffles through LDS cost a
+// round trip each and made the score reduction the kernel's bottleneck.
+template <int LP>
+__device__ __forceinline__ float pos_group_sum(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror: lane i + lane 7-i of each 8
+  if constexpr (LP >= 16) v += dpp_f<0x140>(v);  // row_mirror
+  if constexpr (LP >= 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
+
+__device__ __forceinline__ void unpack8(const uint4 v, float *f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = h2f((uint16_t)(w[i] & 0xFFFFu));
+    f[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+  }
+}
+
 template <int LP, bool ROPE>  // LP = lanes per position = hd / 8
-__global__ __launch_bounds__(256) void attn_decode_kernel(
+__global__ __launch_bounds__(ATTN_THREADS) void attn_decode_kernel(
     const float *__restrict__ qkv, uint16_t *__restrict__ k_cache,
     uint16_t *__restrict__ v_cache, float *__restrict__ partials, uint16_t *__restrict__ out,
     unsigned int *__restrict__ counters, int n_q, int n_kv,
     const int32_t *__restrict__ pos_dev, int max_seq, float scale, int splits, RopeArgs ra) {
   constexpr int HD = LP * 8;
   constexpr int PPW = 64 / LP;  // positions per wave step
+  constexpr int STEP = ATTN_WAVES * PPW * ATTN_UNROLL;  // positions per block iteration
+  constexpr int MAXG = HD > 128 ? 4 : ATTN_MAX_GQA;  // LDS: at most 4 heads at hd 256
   const int gqa = n_q / n_kv;
   const int kvh = blockIdx.x, split = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -80,25 +118,40 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int t0 = split * per;
   const int t1 = min(t0 + per, seq);
 
-  __shared__ float qs[ROPE ? ATTN_MAX_GQA * HD : 1];
+  const uint16_t *kb = k_cache + (size_t)kvh * max_seq * HD;
+  const uint16_t *vb = v_cache + (size_t)kvh * max_seq * HD;
+
+  // First iteration's K/V requests go out before anything else.
+  uint4 kq[ATTN_UNROLL], vq[ATTN_UNROLL];
+  int base = t0 + wave * PPW * ATTN_UNROLL;
+#pragma unroll
+  for (int u = 0; u < ATTN_UNROLL; ++u) {
+    const int t = base + u * PPW + pg;
+    if (t < t1) {
+      kq[u] = *(const uint4 *)(kb + (size_t)t * HD + sub * 8);
+      vq[u] = *(const uint4 *)(vb + (size_t)t * HD + sub * 8);
+    }
+  }
+
+  __shared__ float qs[MAXG * HD];
+  __shared__ uint16_t kv_now[2 * HD];  // ROPE: this position's k and v (f16)
+  const bool owner = ROPE && pos >= t0 && pos < t1;
   if constexpr (ROPE) {
     // One wave per head, as wst_rope_cache runs one 64-thread block per head
     // (hd <= 128): lane j owns elements j and j + hd/2.
-    __shared__ float red[4][16];
     constexpr int HALF = HD / 2;
     const int j = lane;
     const bool active = j < HALF;
     const float c = active ? ra.cos_tab[(size_t)pos * HALF + j] : 0.0f;
     const float s = active ? ra.sin_tab[(size_t)pos * HALF + j] : 0.0f;
-    const bool owner = pos >= t0 && pos < t1;  // this block appends k/v
-    for (int h = wave; h < gqa + 1; h += 4) {
+    for (int h = wave; h < gqa + 1; h += ATTN_WAVES) {
       const bool is_k = h == gqa;
       const float *src = is_k ? qkv + (size_t)(n_q + kvh) * HD : qkv + (size_t)(kvh * gqa + h) * HD;
       float x1 = active ? src[j] : 0.0f;
       float x2 = active ? src[j + HALF] : 0.0f;
       const uint16_t *g = is_k ? ra.k_norm_w : ra.q_norm_w;
       if (g) {
-        // Single-wave form of qk_norm: for one wave block_sum == wave_sum.
+        // Single-wave form of qk_norm: for one wave block_sum == 0 + wave_sum.
         const float a = active ? fmaf(x1, x1, x2 * x2) : 0.0f;
         const float ss = 0.0f + wave_sum(a);
         const float sc = 1.0f / sqrtf(ss / (float)HD + ra.eps);
@@ -113,74 +166,63 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         qs[h * HD + j] = lo;
         qs[h * HD + j + HALF] = hi;
       } else if (owner) {
-        const size_t slot = ((size_t)kvh * max_seq + pos) * HD;
         const float *vh = qkv + (size_t)(n_q + n_kv + kvh) * HD;
-        k_cache[slot + j] = f2h(lo);
-        k_cache[slot + j + HALF] = f2h(hi);
-        v_cache[slot + j] = f2h(vh[j]);
-        v_cache[slot + j + HALF] = f2h(vh[j + HALF]);
+        const uint16_t k1 = f2h(lo), k2 = f2h(hi), v1 = f2h(vh[j]), v2 = f2h(vh[j + HALF]);
+        kv_now[j] = k1;
+        kv_now[j + HALF] = k2;
+        kv_now[HD + j] = v1;
+        kv_now[HD + j + HALF] = v2;
+        const size_t slot = ((size_t)kvh * max_seq + pos) * HD;
+        k_cache[slot + j] = k1;
+        k_cache[slot + j + HALF] = k2;
+        v_cache[slot + j] = v1;
+        v_cache[slot + j + HALF] = v2;
       }
     }
-    (void)red;
-    __syncthreads();
+  } else {
+    for (int k = tid; k < gqa * HD; k += ATTN_THREADS)
+      qs[k] = qkv[(size_t)kvh * gqa * HD + k];
   }
+  __syncthreads();
 
   // q slices for every head of the group, pre-scaled (attention.cu:98-101).
-  float qr[ATTN_MAX_GQA][8];
+  float qr[MAXG][8];
 #pragma unroll
-  for (int h = 0; h < ATTN_MAX_GQA; ++h) {
+  for (int h = 0; h < MAXG; ++h) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = 0.0f;
-      if (h < gqa) v = ROPE ? qs[h * HD + sub * 8 + i] : qkv[(size_t)(kvh * gqa + h) * HD + sub * 8 + i];
-      qr[h][i] = v * scale;
-    }
+    for (int i = 0; i < 8; ++i) qr[h][i] = h < gqa ? qs[h * HD + sub * 8 + i] * scale : 0.0f;
   }
 
-  float m[ATTN_MAX_GQA], l[ATTN_MAX_GQA], acc[ATTN_MAX_GQA][8];
+  float m[MAXG], l[MAXG], acc[MAXG][8];
 #pragma unroll
-  for (int h = 0; h < ATTN_MAX_GQA; ++h) {
+  for (int h = 0; h < MAXG; ++h) {
     m[h] = -INFINITY;
     l[h] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[h][i] = 0.0f;
   }
 
-  // Each wave sweeps ATTN_UNROLL steps of PPW positions per iteration; all the
-  // K/V loads of an iteration are issued before any is consumed.
-  const uint16_t *kb = k_cache + (size_t)kvh * max_seq * HD;
-  const uint16_t *vb = v_cache + (size_t)kvh * max_seq * HD;
-  for (int base = t0 + wave * PPW * ATTN_UNROLL; base < t1; base += 4 * PPW * ATTN_UNROLL) {
-    uint4 kq[ATTN_UNROLL], vq[ATTN_UNROLL];
+  while (base < t1) {
+    const int next = base + STEP;
 #pragma unroll
     for (int u = 0; u < ATTN_UNROLL; ++u) {
       const int t = base + u * PPW + pg;
-      if (t < t1) {
-        kq[u] = *(const uint4 *)(kb + (size_t)t * HD + sub * 8);
-        vq[u] = *(const uint4 *)(vb + (size_t)t * HD + sub * 8);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < ATTN_UNROLL; ++u) {
-      if (base + u * PPW + pg >= t1) continue;  // uniform across the position's lanes
+      if (t >= t1) continue;  // uniform across the position's lanes
       float kf[8], vf[8];
-      const uint32_t kw[4] = {kq[u].x, kq[u].y, kq[u].z, kq[u].w};
-      const uint32_t vw[4] = {vq[u].x, vq[u].y, vq[u].z, vq[u].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        kf[2 * i] = h2f((uint16_t)(kw[i] & 0xFFFFu));
-        kf[2 * i + 1] = h2f((uint16_t)(kw[i] >> 16));
-        vf[2 * i] = h2f((uint16_t)(vw[i] & 0xFFFFu));
-        vf[2 * i + 1] = h2f((uint16_t)(vw[i] >> 16));
+      if (owner && t == pos) {
+        unpack8(*(const uint4 *)(kv_now + sub * 8), kf);
+        unpack8(*(const uint4 *)(kv_now + HD + sub * 8), vf);
+      } else {
+        unpack8(kq[u], kf);
+        unpack8(vq[u], vf);
       }
 #pragma unroll
-      for (int h = 0; h < ATTN_MAX_GQA; ++h) {
+      for (int h = 0; h < MAXG; ++h) {
         if (h >= gqa) break;
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) s = fmaf(qr[h][i], kf[i], s);
-#pragma unroll
-        for (int o = 1; o < LP; o <<= 1) s += __shfl_xor(s, o, 64);
+        s = pos_group_sum<LP>(s);
         const float mn = fmaxf(m[h], s);
         const float corr = __expf(m[h] - mn);
         const float p = __expf(s - mn);
@@ -190,13 +232,24 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         m[h] = mn;
       }
     }
+    base = next;
+    if (base < t1) {
+#pragma unroll
+      for (int u = 0; u < ATTN_UNROLL; ++u) {
+        const int t = base + u * PPW + pg;
+        if (t < t1) {
+          kq[u] = *(const uint4 *)(kb + (size_t)t * HD + sub * 8);
+          vq[u] = *(const uint4 *)(vb + (size_t)t * HD + sub * 8);
+        }
+      }
+    }
   }
 
   // Merge the position groups of this wave (lanes with equal `sub`).
 #pragma unroll
   for (int o = LP; o < 64; o <<= 1) {
 #pragma unroll
-    for (int h = 0; h < ATTN_MAX_GQA; ++h) {
+    for (int h = 0; h < MAXG; ++h) {
       if (h >= gqa) break;
       const float mo = __shfl_xor(m[h], o, 64);
       const float lo = __shfl_xor(l[h], o, 64);
@@ -207,13 +260,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
   }
 
-  // Merge the 4 waves through LDS: [wave][head][HD + 2].
-  __shared__ float sm[4 * ATTN_MAX_GQA * (HD + 2)];
+  // Merge the waves through LDS: [wave][head][HD + 2].
+  __shared__ float sm[ATTN_WAVES * MAXG * (HD + 2)];
   if (pg == 0) {
 #pragma unroll
-    for (int h = 0; h < ATTN_MAX_GQA; ++h) {
+    for (int h = 0; h < MAXG; ++h) {
       if (h >= gqa) break;
-      float *e = sm + (wave * ATTN_MAX_GQA + h) * (HD + 2);
+      float *e = sm + (wave * MAXG + h) * (HD + 2);
       if (sub == 0) {
         e[0] = m[h];
         e[1] = l[h];
@@ -227,15 +280,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   // This slice's partial: acc [n_q][splits][HD], then (m, l) [n_q][splits][2].
   float *pacc = partials;
   float *pml = partials + (size_t)n_q * splits * HD;
-  for (int k = tid; k < gqa * HD; k += 256) {
+  for (int k = tid; k < gqa * HD; k += ATTN_THREADS) {
     const int h = k / HD, d = k % HD;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[(w * ATTN_MAX_GQA + h) * (HD + 2)]);
+    for (int w = 0; w < ATTN_WAVES; ++w) M = fmaxf(M, sm[(w * MAXG + h) * (HD + 2)]);
     float num = 0.0f, den = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float *e = sm + (w * ATTN_MAX_GQA + h) * (HD + 2);
+    for (int w = 0; w < ATTN_WAVES; ++w) {
+      const float *e = sm + (w * MAXG + h) * (HD + 2);
       const float f = (e[0] == -INFINITY) ? 0.0f : __expf(e[0] - M);
       num = fmaf(e[2 + d], f, num);
       den = fmaf(e[1], f, den);
@@ -250,46 +303,38 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 
   if (!last_block_done(counters + kvh, (unsigned int)splits)) return;
 
-  // Slice merge for the gqa heads of this kv head (attention.cu:170-193), in
-  // three parallel phases so no thread walks the slices with dependent loads:
-  // (1) every (head, slice) max/denominator into LDS, (2) per head the global
-  // max, the slice weights and the denominator, (3) per (head, 4 dims) the
-  // weighted sum of the slice numerators, float4 loads unrolled.
-  __shared__ float fsh[ATTN_MAX_GQA * ATTN_MAX_SPLITS], lsh[ATTN_MAX_GQA * ATTN_MAX_SPLITS];
-  __shared__ float densh[ATTN_MAX_GQA];
-  for (int k = tid; k < gqa * splits; k += 256) {
-    const size_t row = (size_t)kvh * gqa * splits + k;  // == (kvh*gqa + h)*splits + s
-    fsh[k] = pml[row * 2];
-    lsh[k] = pml[row * 2 + 1];
-  }
-  __syncthreads();
-  if (tid < gqa) {
-    const float *mh = fsh + tid * splits;
-    float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) M = fmaxf(M, mh[s]);
-    float den = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-      const float f = (mh[s] == -INFINITY) ? 0.0f : __expf(mh[s] - M);
-      den = fmaf(lsh[tid * splits + s], f, den);
-      fsh[tid * splits + s] = f;
-    }
-    densh[tid] = den;
-  }
-  __syncthreads();
-  for (int k = tid; k < gqa * (HD / 4); k += 256) {
+  // Slice merge for the gqa heads of this kv head (attention.cu:170-193): one
+  // thread per (head, 4 dims) fetches all slices' (m, l) and numerators in one
+  // batch, then combines them in slice order.
+  for (int k = tid; k < gqa * (HD / 4); k += ATTN_THREADS) {
     const int h = k / (HD / 4), d4 = k % (HD / 4);
-    const float4 *src = (const float4 *)(pacc + (size_t)(kvh * gqa + h) * splits * HD) + d4;
-    const float *f = fsh + h * splits;
-    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 8
-    for (int s = 0; s < splits; ++s) {
-      const float4 v = src[(size_t)s * (HD / 4)];
-      a.x = fmaf(v.x, f[s], a.x);
-      a.y = fmaf(v.y, f[s], a.y);
-      a.z = fmaf(v.z, f[s], a.z);
-      a.w = fmaf(v.w, f[s], a.w);
+    const size_t row0 = (size_t)(kvh * gqa + h) * splits;
+    float ms[ATTN_MAX_SPLITS], ls[ATTN_MAX_SPLITS];
+    float4 vs[ATTN_MAX_SPLITS];
+#pragma unroll
+    for (int s = 0; s < ATTN_MAX_SPLITS; ++s) {
+      if (s < splits) {
+        ms[s] = pml[(row0 + s) * 2];
+        ls[s] = pml[(row0 + s) * 2 + 1];
+        vs[s] = ((const float4 *)(pacc + (row0 + s) * HD))[d4];
+      }
     }
-    const float den = densh[h];
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
+      if (s < splits) M = fmaxf(M, ms[s]);
+    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float den = 0.0f;
+#pragma unroll
+    for (int s = 0; s < ATTN_MAX_SPLITS; ++s) {
+      if (s >= splits) break;
+      const float f = (ms[s] == -INFINITY) ? 0.0f : __expf(ms[s] - M);
+      a.x = fmaf(vs[s].x, f, a.x);
+      a.y = fmaf(vs[s].y, f, a.y);
+      a.z = fmaf(vs[s].z, f, a.z);
+      a.w = fmaf(vs[s].w, f, a.w);
+      den = fmaf(ls[s], f, den);
+    }
     uint16_t *o = out + (size_t)(kvh * gqa + h) * HD + d4 * 4;
     o[0] = f2h(a.x / den);
     o[1] = f2h(a.y / den);
@@ -305,7 +350,7 @@ static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_ca
                         const RopeArgs &ra) {
   const dim3 grid(n_kv, splits);
 #define WST_ATTN_GO(LP)                                                                     \
-  attn_decode_kernel<LP, ROPE><<<grid, 256, 0, WST_STREAM>>>(                               \
+  attn_decode_kernel<LP, ROPE><<<grid, ATTN_THREADS, 0, WST_STREAM>>>(                      \
       (const float *)qkv, (uint16_t *)k_cache, (uint16_t *)v_cache, (float *)partials,      \
       (uint16_t *)out, counters, n_q, n_kv, (const int32_t *)pos, max_seq, scale, splits, ra)
   switch (head_dim) {
@@ -334,12 +379,14 @@ static wst_status_t attn_check(const void *q, const void *k_cache, const void *v
               "wst_attn_decode: query heads must be a multiple of key/value heads");
   WST_REQUIRE(n_q / n_kv <= ATTN_MAX_GQA,
               "wst_attn_decode: more than 8 query heads per kv head");
+  WST_REQUIRE(head_dim != 256 || n_q / n_kv <= 4,
+              "wst_attn_decode: head_dim 256 supports at most 4 query heads per kv head");
   WST_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
               "wst_attn_decode: head_dim must be 64, 128 or 256");
   WST_REQUIRE(max_seq > 0, "wst_attn_decode: empty cache");
   WST_REQUIRE(n_kv <= 4096, "wst_attn_decode: too many kv heads");
-  WST_REQUIRE(!(((uintptr_t)k_cache | (uintptr_t)v_cache) & 15u),
-              "wst_attn_decode: caches must be 16-byte aligned");
+  WST_REQUIRE(!(((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)partials) & 15u),
+              "wst_attn_decode: caches and partials must be 16-byte aligned");
   return WST_OK;
 }
 

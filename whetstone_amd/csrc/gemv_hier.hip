@@ -10,37 +10,39 @@
 // How it maps onto CDNA4
 // ----------------------
 // * One lane owns whole groups: a group is 16 bytes of nibbles, exactly one
-//   dwordx4 load, and a row-slot of LPR consecutive lanes reads a contiguous
-//   run of the row. A wave therefore issues 1 KB-wide coalesced loads, and
-//   each lane keeps TILE*NG of them in flight before it does any arithmetic.
-// * x is staged once per block in LDS (normalised there when the RMSNorm is
-//   fused), then each lane's slice (64 B per group) moves into registers for
-//   the rest of the kernel: no LDS traffic in the inner loop. The grid is
-//   persistent (a few blocks per CU) so the staging is paid a few times per CU,
-//   not once per row. x is permuted so that the nibble pairs produced by one
-//   bit-field insert line up with the x pairs they multiply.
+//   dwordx4 load, and a row-slot of 64 consecutive lanes (32 when a row has at
+//   most 32 groups) reads a contiguous run of the row. A wave therefore issues
+//   1 KB-wide coalesced loads. Waves are independent (no barriers after the
+//   prologue) and the kernel is kept near 64 VGPRs so 8 waves share a SIMD:
+//   at this size occupancy, not per-wave prefetch depth, is what keeps enough
+//   bytes in flight to stream HBM3E (measured: 5.9 TB/s of 8 on the 7B
+//   gate|up shape with this arithmetic, vs 4 TB/s at 100+ VGPRs).
+// * x lives in LDS as a per-group table prepared once per block: the 32
+//   activations of a group, permuted so that the nibble pairs produced by one
+//   bit-field insert line up with the activation pairs they multiply, plus the
+//   group's two correction sums. Entries are 80 bytes apart, which keeps a
+//   wave's ds_read_b128 free of bank conflicts.
 // * Unpack without conversions: inserting a nibble into the mantissa of f16
 //   1024.0 gives 1024+q exactly; nibbles in bits 4..7 give 1024+16q. One
 //   v_bfi_b32 per pair of weights, one shift per word, and v_dot2c_f32_f16
-//   multiplies two of them by two activations with an f32 accumulator. The
-//   1024 offsets are removed once per group with per-group sums of x computed
-//   at start-up:
+//   multiplies two of them by two activations with an f32 accumulator:
 //       sum_i q_i x_i = DA + DB/16 - (1024*sum_even x + 64*sum_odd x)
 //   where DA (DB) accumulates the even (odd) columns. About 1.1 VALU
-//   instructions per weight, and every product is accumulated in f32 -- more
-//   precise than the reference's f16 half2 accumulation inside a group.
+//   instructions per weight, every product accumulated in f32 -- more precise
+//   than the reference's f16 half2 accumulation inside a group.
 // * Per row: y = d * sum_g ls_g*Q_g - dmin * sum_g lm_g*S_g, reduced across the
-//   row-slot with DPP row operations and, for rows split over several waves,
-//   through LDS in a fixed order. Results are deterministic and do not depend
-//   on TILE, the grid, or which fused form ran: a row's value is a function of
-//   (in_f, the row's bytes, x) only. That is what lets the fused kernels be
-//   checked bit for bit against the unfused ABI sequence.
+//   row-slot with DPP. A row's value depends only on (in_f, the row's bytes,
+//   x): not on TILE, the grid, or which fused form ran, so the fused kernels
+//   can be checked bit for bit against the unfused ABI sequence.
 #include "common.hpp"
 
 #include <stdlib.h>
 
 #define HGROUP 32
 #define HIER_MAGIC 0x64006400u  // f16 1024.0 in both halves
+#define GEMV_THREADS 512
+#define XG_WORDS 20      // LDS words per group entry (18 used)
+#define GEMV_MAX_G 768   // groups per row handled by the LDS-table kernel
 
 // Bit-field insert (a & m) | (b & ~m) as one v_bfi_b32: the mask lives in a
 // VGPR and the magic constant in an SGPR kernel argument. (Left to itself the
@@ -51,8 +53,7 @@ __device__ __forceinline__ uint32_t bfi(uint32_t a, uint32_t m, uint32_t b) {
   return r;
 }
 
-// A lane's resident slice of x for one group: the permuted activation pairs
-// and the two correction terms.
+// A group's activations as the unpack consumes them.
 struct XGroup {
   uint32_t ea[4], ob[4], ea2[4], ob2[4];  // (x0,x4) (x1,x5) (x2,x6) (x3,x7) per word
   float corr;                             // 1024*sum_even + 64*sum_odd
@@ -79,18 +80,25 @@ __device__ __forceinline__ void build_xgroup(const uint32_t r[16], XGroup &xg) {
   xg.sum = se + so;
 }
 
-__device__ __forceinline__ void load_xgroup(const uint16_t *__restrict__ x, int g, XGroup &xg) {
-  const uint4 *xv = (const uint4 *)(x + (size_t)g * HGROUP);
-  uint32_t r[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint4 v = xv[i];
-    r[4 * i + 0] = v.x;
-    r[4 * i + 1] = v.y;
-    r[4 * i + 2] = v.z;
-    r[4 * i + 3] = v.w;
-  }
-  build_xgroup(r, xg);
+__device__ __forceinline__ void store_xgroup(uint32_t *e, const XGroup &xg) {
+  uint4 *v = (uint4 *)e;
+  v[0] = make_uint4(xg.ea[0], xg.ea[1], xg.ea[2], xg.ea[3]);
+  v[1] = make_uint4(xg.ob[0], xg.ob[1], xg.ob[2], xg.ob[3]);
+  v[2] = make_uint4(xg.ea2[0], xg.ea2[1], xg.ea2[2], xg.ea2[3]);
+  v[3] = make_uint4(xg.ob2[0], xg.ob2[1], xg.ob2[2], xg.ob2[3]);
+  e[16] = __float_as_uint(xg.corr);
+  e[17] = __float_as_uint(xg.sum);
+}
+
+__device__ __forceinline__ void load_xgroup_lds(const uint32_t *e, XGroup &xg) {
+  const uint4 *v = (const uint4 *)e;
+  const uint4 a = v[0], b = v[1], c = v[2], d = v[3];
+  xg.ea[0] = a.x; xg.ea[1] = a.y; xg.ea[2] = a.z; xg.ea[3] = a.w;
+  xg.ob[0] = b.x; xg.ob[1] = b.y; xg.ob[2] = b.z; xg.ob[3] = b.w;
+  xg.ea2[0] = c.x; xg.ea2[1] = c.y; xg.ea2[2] = c.z; xg.ea2[3] = c.w;
+  xg.ob2[0] = d.x; xg.ob2[1] = d.y; xg.ob2[2] = d.z; xg.ob2[3] = d.w;
+  xg.corr = __uint_as_float(e[16]);
+  xg.sum = __uint_as_float(e[17]);
 }
 
 // sum_i q_i x_i for one packed group (32 nibbles in `p`) against `xg`.
@@ -116,65 +124,103 @@ __device__ __forceinline__ float slot_sum(float v) {
 
 // ---------------------------------------------------------------- the kernel
 //
-// LPR lanes cooperate on a row (32, 64, 128 or 256); each owns NG groups of
-// the row (group g = lane_in_row + j*LPR). A unit of work is TILE rows per
-// row-slot. Blocks are 256 threads. For LPR <= 64 waves are independent; for
-// LPR > 64 the W = LPR/64 waves of a row combine through LDS.
+// LPR (32 or 64) lanes own a row; lane lr holds groups lr, lr+LPR, ... (NG of
+// them). A unit is TILE rows per row-slot; units are handed to waves
+// round-robin over the whole grid, so after the prologue every wave runs on
+// its own.
 //
-// NORM:   x is the f32 residual stream; every block computes its RMS scale and
-//         normalises with norm_w on the fly (wst_rmsnorm + GEMV). Block 0
-//         also stores h when h_out is non-null.
+// NORM:   x is the f32 residual stream; the prologue computes the RMS scale
+//         (the same reduction as the RMSNorm kernel) and normalises with
+//         norm_w while building the table (wst_rmsnorm + GEMV). Block 0 also
+//         stores h when h_out is non-null.
 // SWIGLU: out_f is the intermediate width; unit row r computes gate row r and
 //         up row r + out_f of the fused matrix and writes f16(silu(g) * u)
 //         (GEMV + wst_swiglu).
 template <int LPR, int NG, int TILE, bool NORM, bool SWIGLU>
-__global__ __launch_bounds__(256) void gemv_hier_kernel(
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_hier_kernel(
     const uint4 *__restrict__ qw, const uint8_t *__restrict__ si,
     const uint32_t *__restrict__ sb, const void *__restrict__ xin,
     const uint16_t *__restrict__ norm_w, float eps, uint16_t *__restrict__ h_out,
     const uint16_t *__restrict__ bias, void *__restrict__ yout, int in_f, int out_f, int accum,
     uint32_t magic) {
-  constexpr int SLOTS = 256 / LPR;  // row-slots per block
-  constexpr int W = LPR > 64 ? LPR / 64 : 1;
+  constexpr int SLOTS = 64 / LPR;    // row-slots per wave
   constexpr int NR = SWIGLU ? 2 : 1;  // matrix rows per unit row
-  const int tid = threadIdx.x;
-  const int slot = tid / LPR, lr = tid % LPR;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int slot = lane / LPR, lr = lane % LPR;
   const int G = in_f / HGROUP;
 
   __shared__ float red[16];
-  __shared__ float wred[4][TILE * NR];
-  // The activation vector, staged once per block (f16, in_f entries): every
-  // row-slot builds its register slices from here instead of each re-reading
-  // x from L2.
-  extern __shared__ uint4 xs_raw[];
-  uint16_t *xs = (uint16_t *)xs_raw;
+  extern __shared__ uint32_t xgt[];  // [G][XG_WORDS]
 
+  // ---- prologue: the x table
+  float s = 0.0f;
   if constexpr (NORM) {
+    // rms_scale256's reduction, spread over 512 threads with the upper 256
+    // contributing exact zeros: same bits as the RMSNorm kernel.
+    // The first 16 strided values are loaded together (one round trip), then
+    // accumulated in index order.
     const float *x = (const float *)xin;
-    const float s = rms_scale256(x, in_f, eps, red);
-    for (int i = tid; i < in_f; i += 256) xs[i] = f2h(x[i] * s * h2f(norm_w[i]));
-  } else {
-    const uint4 *x = (const uint4 *)xin;
-    for (int i = tid; i < in_f / 8; i += 256) xs_raw[i] = x[i];
+    float acc = 0.0f;
+    if (tid < 256) {
+      float v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int i = tid + 256 * k;
+        v[k] = i < in_f ? x[i] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (tid + 256 * k < in_f) acc = fmaf(v[k], v[k], acc);
+      for (int i = tid + 256 * 16; i < in_f; i += 256) acc = fmaf(x[i], x[i], acc);
+    }
+    s = 1.0f / sqrtf(block_sum(acc, red) / (float)in_f + eps);
+  }
+  for (int g = tid; g < G; g += GEMV_THREADS) {
+    uint32_t r[16];
+    if constexpr (NORM) {
+      const float4 *xv = (const float4 *)((const float *)xin + (size_t)g * HGROUP);
+      const uint4 *wv = (const uint4 *)(norm_w + (size_t)g * HGROUP);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 a = xv[2 * i], b = xv[2 * i + 1];
+        const uint4 ww = wv[i];
+        const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const uint32_t wp[4] = {ww.x, ww.y, ww.z, ww.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint16_t lo = f2h(xs[2 * k] * s * h2f((uint16_t)(wp[k] & 0xFFFFu)));
+          const uint16_t hi = f2h(xs[2 * k + 1] * s * h2f((uint16_t)(wp[k] >> 16)));
+          r[4 * i + k] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+      }
+      if (h_out && blockIdx.x == 0) {
+        uint4 *hv = (uint4 *)(h_out + (size_t)g * HGROUP);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          hv[i] = make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+      }
+    } else {
+      const uint4 *xv = (const uint4 *)((const uint16_t *)xin + (size_t)g * HGROUP);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = xv[i];
+        r[4 * i] = v.x;
+        r[4 * i + 1] = v.y;
+        r[4 * i + 2] = v.z;
+        r[4 * i + 3] = v.w;
+      }
+    }
+    XGroup xg;
+    build_xgroup(r, xg);
+    store_xgroup(xgt + (size_t)g * XG_WORDS, xg);
   }
   __syncthreads();
-  if (NORM && h_out && blockIdx.x == 0)
-    for (int i = tid; i < in_f / 8; i += 256) ((uint4 *)h_out)[i] = xs_raw[i];
 
-  XGroup xg[NG];
-  bool gv[NG];
-#pragma unroll
-  for (int j = 0; j < NG; ++j) {
-    const int g = lr + j * LPR;
-    gv[j] = g < G;
-    if (gv[j]) load_xgroup(xs, g, xg[j]);
-  }
-
-  const int rows_per_block = SLOTS * TILE;
-  const int nunits = (out_f + rows_per_block - 1) / rows_per_block;
-  for (int unit = blockIdx.x; unit < nunits; unit += gridDim.x) {
-    const int row0 = unit * rows_per_block + slot * TILE;
-
+  // ---- rows
+  const int nunits = (out_f + SLOTS * TILE - 1) / (SLOTS * TILE);
+  const int tw = gridDim.x * (GEMV_THREADS / 64);
+  for (int unit = blockIdx.x * (GEMV_THREADS / 64) + (tid >> 6); unit < nunits; unit += tw) {
+    const int row0 = (unit * SLOTS + slot) * TILE;
     uint4 wq[TILE][NR][NG];
     uint32_t idx[TILE][NR][NG];
     uint32_t sbv[TILE][NR];
@@ -187,8 +233,9 @@ __global__ __launch_bounds__(256) void gemv_hier_kernel(
         sbv[t][k] = rv ? sb[r] : 0u;
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
-          const size_t at = (size_t)r * G + lr + j * LPR;
-          if (rv && gv[j]) {
+          const int g = lr + j * LPR;
+          const size_t at = (size_t)r * G + g;
+          if (rv && g < G) {
             wq[t][k][j] = ld_stream16(qw + at);
             idx[t][k][j] = si[at];
           } else {
@@ -198,58 +245,42 @@ __global__ __launch_bounds__(256) void gemv_hier_kernel(
         }
       }
     }
-
-    float part[TILE][NR];
+    float as[TILE][NR], am[TILE][NR];
+#pragma unroll
+    for (int t = 0; t < TILE; ++t)
+#pragma unroll
+      for (int k = 0; k < NR; ++k) as[t][k] = am[t][k] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int g = lr + j * LPR;
+      if (g >= G) continue;
+      XGroup xg;
+      load_xgroup_lds(xgt + (size_t)g * XG_WORDS, xg);
+#pragma unroll
+      for (int t = 0; t < TILE; ++t)
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+          const float q = group_dot(wq[t][k][j], xg, magic);
+          as[t][k] = fmaf((float)(idx[t][k][j] & 0xFu), q, as[t][k]);
+          am[t][k] = fmaf((float)(idx[t][k][j] >> 4), xg.sum, am[t][k]);
+        }
+    }
 #pragma unroll
     for (int t = 0; t < TILE; ++t) {
+      float part[NR];
 #pragma unroll
       for (int k = 0; k < NR; ++k) {
-        float as = 0.0f, am = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NG; ++j) {
-          if (!gv[j]) continue;
-          const float q = group_dot(wq[t][k][j], xg[j], magic);
-          as = fmaf((float)(idx[t][k][j] & 0xFu), q, as);
-          am = fmaf((float)(idx[t][k][j] >> 4), xg[j].sum, am);
-        }
         const float d = h2f((uint16_t)(sbv[t][k] & 0xFFFFu));
         const float dm = h2f((uint16_t)(sbv[t][k] >> 16));
-        part[t][k] = slot_sum<LPR>(d * as - dm * am);
+        part[k] = slot_sum<LPR>(d * as[t][k] - dm * am[t][k]);
       }
-    }
-
-    if constexpr (W > 1) {
-      const int wave = tid >> 6;
-      if ((tid & 63) == 0) {
-#pragma unroll
-        for (int t = 0; t < TILE; ++t)
-#pragma unroll
-          for (int k = 0; k < NR; ++k) wred[wave][t * NR + k] = part[t][k];
-      }
-      __syncthreads();
-      if ((tid & 63) == 0 && (wave % W) == 0) {
-#pragma unroll
-        for (int t = 0; t < TILE; ++t)
-#pragma unroll
-          for (int k = 0; k < NR; ++k) {
-            float v = 0.0f;
-            for (int q = 0; q < W; ++q) v += wred[wave + q][t * NR + k];  // fixed order
-            part[t][k] = v;
-          }
-      }
-      __syncthreads();  // `wred` is reused by the next unit
-    }
-
-    if (lr == 0) {
-#pragma unroll
-      for (int t = 0; t < TILE; ++t) {
-        const int r = row0 + t;
-        if (r >= out_f) continue;
+      const int r = row0 + t;
+      if (lr == 0 && r < out_f) {
         if constexpr (SWIGLU) {
-          const float g = part[t][0], u = part[t][1];
-          ((uint16_t *)yout)[r] = f2h(g / (1.0f + __expf(-g)) * u);
+          const float g = part[0], up = part[NR - 1];
+          ((uint16_t *)yout)[r] = f2h(g / (1.0f + __expf(-g)) * up);
         } else {
-          float v = part[t][0];
+          float v = part[0];
           if (bias) v += h2f(bias[r]);
           float *y = (float *)yout;
           y[r] = accum ? y[r] + v : v;
@@ -259,8 +290,8 @@ __global__ __launch_bounds__(256) void gemv_hier_kernel(
   }
 }
 
-// Fallback for rows wider than 28672 columns: x is re-read from L2 per group
-// rather than held in registers. Same arithmetic per group; plain GEMV only.
+// Fallback for rows wider than GEMV_MAX_G groups: x is re-read from L2 per
+// group. Same arithmetic per group; plain GEMV only.
 template <int TILE>
 __global__ __launch_bounds__(256) void gemv_hier_wide_kernel(
     const uint4 *__restrict__ qw, const uint8_t *__restrict__ si,
@@ -276,13 +307,23 @@ __global__ __launch_bounds__(256) void gemv_hier_wide_kernel(
 #pragma unroll
     for (int t = 0; t < TILE; ++t) as[t] = am[t] = 0.0f;
     for (int g = tid; g < G; g += 256) {
+      uint32_t r[16];
+      const uint4 *xv = (const uint4 *)(x + (size_t)g * HGROUP);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = xv[i];
+        r[4 * i] = v.x;
+        r[4 * i + 1] = v.y;
+        r[4 * i + 2] = v.z;
+        r[4 * i + 3] = v.w;
+      }
       XGroup xg;
-      load_xgroup(x, g, xg);
+      build_xgroup(r, xg);
 #pragma unroll
       for (int t = 0; t < TILE; ++t) {
-        const int r = row0 + t;
-        if (r >= out_f) continue;
-        const size_t at = (size_t)r * G + g;
+        const int rr = row0 + t;
+        if (rr >= out_f) continue;
+        const size_t at = (size_t)rr * G + g;
         const uint32_t id = si[at];
         const float q = group_dot(ld_stream16(qw + at), xg, magic);
         as[t] = fmaf((float)(id & 0xFu), q, as[t]);
@@ -292,8 +333,8 @@ __global__ __launch_bounds__(256) void gemv_hier_wide_kernel(
     float part[TILE];
 #pragma unroll
     for (int t = 0; t < TILE; ++t) {
-      const int r = row0 + t < out_f ? row0 + t : out_f - 1;
-      const uint32_t sv = sb[r];
+      const int rr = row0 + t < out_f ? row0 + t : out_f - 1;
+      const uint32_t sv = sb[rr];
       part[t] = wave_sum(h2f((uint16_t)(sv & 0xFFFFu)) * as[t] - h2f((uint16_t)(sv >> 16)) * am[t]);
     }
     if ((tid & 63) == 0)
@@ -303,11 +344,11 @@ __global__ __launch_bounds__(256) void gemv_hier_wide_kernel(
     if (tid == 0) {
 #pragma unroll
       for (int t = 0; t < TILE; ++t) {
-        const int r = row0 + t;
-        if (r >= out_f) continue;
+        const int rr = row0 + t;
+        if (rr >= out_f) continue;
         float v = red[0][t] + red[1][t] + red[2][t] + red[3][t];
-        if (bias) v += h2f(bias[r]);
-        y[r] = accum ? y[r] + v : v;
+        if (bias) v += h2f(bias[rr]);
+        y[rr] = accum ? y[rr] + v : v;
       }
     }
     __syncthreads();
@@ -317,9 +358,10 @@ __global__ __launch_bounds__(256) void gemv_hier_wide_kernel(
 // ---------------------------------------------------------------- dispatch
 
 // Tile rule (wide reduction, huge output, everything else), entries 0..3 ->
-// TILE 1, 2, 4, 8 rows per row-slot. Same knob and classes as the reference
+// TILE 1, 2, 4, 8 rows per row-slot, clamped so a lane holds at most 16
+// groups per unit. Same knob and classes as the reference
 // (gemv_hier.cu:253-272); the defaults are this kernel's own.
-static int g_hier_rule[3] = {1, 2, 2};
+static int g_hier_rule[3] = {0, 0, 1};
 
 extern "C" void wst_gemv_hier_set_rule(int32_t wide, int32_t huge, int32_t other) {
   if (wide >= 0 && wide < 4) g_hier_rule[0] = wide;
@@ -340,18 +382,8 @@ static int hier_tile_index(int in_f, int rows) {
   return g_hier_rule[2];
 }
 
-struct HierArgs {
-  const void *qw, *si, *sb, *x;
-  const void *norm_w;
-  float eps;
-  void *h_out;
-  const void *bias;
-  void *y;
-  int in_f, out_f, accum;
-};
-
-// Persistent grid: a few blocks per CU stream every row; each block stages x
-// once. WST_GEMV_BLOCKS_PER_CU overrides the default (for sweeps).
+// Blocks per CU of the persistent grid. WST_GEMV_BLOCKS_PER_CU overrides the
+// default (for sweeps).
 static int blocks_per_cu() {
   static int v = 0;
   if (v == 0) {
@@ -362,14 +394,25 @@ static int blocks_per_cu() {
   return v;
 }
 
+struct HierArgs {
+  const void *qw, *si, *sb, *x;
+  const void *norm_w;
+  float eps;
+  void *h_out;
+  const void *bias;
+  void *y;
+  int in_f, out_f, accum;
+};
+
 template <int LPR, int NG, int TILE, bool NORM, bool SWIGLU>
 static void launch_t(const HierArgs &a) {
-  const int rows_per_block = (256 / LPR) * TILE;
-  const int units = (a.out_f + rows_per_block - 1) / rows_per_block;
+  const int rows_per_wave = (64 / LPR) * TILE;
+  const int units = (a.out_f + rows_per_wave - 1) / rows_per_wave;
+  const int blocks = (units + GEMV_THREADS / 64 - 1) / (GEMV_THREADS / 64);
   const int cap = wst_cu_count() * blocks_per_cu();
-  const int grid = units < cap ? units : cap;
-  const size_t lds = (size_t)a.in_f * 2;
-  gemv_hier_kernel<LPR, NG, TILE, NORM, SWIGLU><<<grid, 256, lds, WST_STREAM>>>(
+  const int grid = blocks < cap ? blocks : cap;
+  const size_t lds = (size_t)(a.in_f / HGROUP) * XG_WORDS * 4;
+  gemv_hier_kernel<LPR, NG, TILE, NORM, SWIGLU><<<grid, GEMV_THREADS, lds, WST_STREAM>>>(
       (const uint4 *)a.qw, (const uint8_t *)a.si, (const uint32_t *)a.sb, a.x,
       (const uint16_t *)a.norm_w, a.eps, (uint16_t *)a.h_out, (const uint16_t *)a.bias, a.y,
       a.in_f, a.out_f, a.accum, HIER_MAGIC);
@@ -377,27 +420,31 @@ static void launch_t(const HierArgs &a) {
 
 template <int LPR, int NG, bool NORM, bool SWIGLU>
 static void launch_tile(int tile_idx, const HierArgs &a) {
-  switch (tile_idx) {
+  constexpr int NR = SWIGLU ? 2 : 1;
+  int t = tile_idx;
+  while (t > 0 && (1 << t) * NG * NR > 16) --t;  // register budget
+  switch (t) {
     case 0: launch_t<LPR, NG, 1, NORM, SWIGLU>(a); break;
-    case 1: launch_t<LPR, NG, 2, NORM, SWIGLU>(a); break;
-    case 3: launch_t<LPR, NG, 8, NORM, SWIGLU>(a); break;
-    default: launch_t<LPR, NG, 4, NORM, SWIGLU>(a); break;
+    case 1: if constexpr (2 * NG * NR <= 16) launch_t<LPR, NG, 2, NORM, SWIGLU>(a); break;
+    case 2: if constexpr (4 * NG * NR <= 16) launch_t<LPR, NG, 4, NORM, SWIGLU>(a); break;
+    default: if constexpr (8 * NG * NR <= 16) launch_t<LPR, NG, 8, NORM, SWIGLU>(a); break;
   }
 }
 
-// Shape -> (lanes per row, groups per lane): at most 3 groups (48 VGPRs of x)
-// per lane up to in_f = 24576, 4 up to 28672 (the staged x is in_f*2 bytes of
-// LDS; past that the wide kernel reads x from L2).
+// Shape -> (lanes per row, groups per lane).
 template <bool NORM, bool SWIGLU>
 static bool hier_dispatch(int tile_idx, const HierArgs &a) {
   const int G = a.in_f / HGROUP;
+  const int ng = (G + 63) / 64;
   if (G <= 32) launch_tile<32, 1, NORM, SWIGLU>(tile_idx, a);
-  else if (G <= 64) launch_tile<64, 1, NORM, SWIGLU>(tile_idx, a);
-  else if (G <= 128) launch_tile<64, 2, NORM, SWIGLU>(tile_idx, a);
-  else if (G <= 192) launch_tile<64, 3, NORM, SWIGLU>(tile_idx, a);
-  else if (G <= 384) launch_tile<128, 3, NORM, SWIGLU>(tile_idx, a);
-  else if (G <= 768) launch_tile<256, 3, NORM, SWIGLU>(tile_idx, a);
-  else if (G <= 896) launch_tile<256, 4, NORM, SWIGLU>(tile_idx, a);
+  else if (ng == 1) launch_tile<64, 1, NORM, SWIGLU>(tile_idx, a);
+  else if (ng == 2) launch_tile<64, 2, NORM, SWIGLU>(tile_idx, a);
+  else if (ng == 3) launch_tile<64, 3, NORM, SWIGLU>(tile_idx, a);
+  else if (ng == 4) launch_tile<64, 4, NORM, SWIGLU>(tile_idx, a);
+  else if (ng <= 6) launch_tile<64, 6, NORM, SWIGLU>(tile_idx, a);
+  else if (ng <= 8) launch_tile<64, 8, NORM, SWIGLU>(tile_idx, a);
+  else if (ng <= 10) launch_tile<64, 10, NORM, SWIGLU>(tile_idx, a);
+  else if (ng <= 12) launch_tile<64, 12, NORM, SWIGLU>(tile_idx, a);
   else return false;
   return true;
 }
@@ -430,7 +477,7 @@ extern "C" wst_status_t wst_gemv_int4_hier_ex(const void *qw, const void *si, co
   const wst_status_t st = check_common(qw, si, sb, x, y, in_f, out_f, "wst_gemv_int4_hier");
   if (st != WST_OK) return st;
   const HierArgs a{qw, si, sb, x, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum};
-  if (!hier_dispatch<false, false>(hier_tile_index(in_f, out_f), a)) {
+  if (in_f / HGROUP > GEMV_MAX_G || !hier_dispatch<false, false>(hier_tile_index(in_f, out_f), a)) {
     const int units = (out_f + 3) / 4;
     const int cap = wst_cu_count() * 16;
     gemv_hier_wide_kernel<4><<<units < cap ? units : cap, 256, 0, WST_STREAM>>>(
@@ -448,7 +495,7 @@ extern "C" wst_status_t wst_gemv_hier_rmsnorm(const void *qw, const void *si, co
   const wst_status_t st = check_common(qw, si, sb, x, y, in_f, out_f, "wst_gemv_hier_rmsnorm");
   if (st != WST_OK) return st;
   WST_REQUIRE(norm_w, "wst_gemv_hier_rmsnorm: null norm weight");
-  WST_REQUIRE(in_f <= 28672, "wst_gemv_hier_rmsnorm: in_features above 28672");
+  WST_REQUIRE(in_f / HGROUP <= GEMV_MAX_G, "wst_gemv_hier_rmsnorm: in_features above 24576");
   WST_REQUIRE(!(((uintptr_t)norm_w | (uintptr_t)h_out) & 15u),
               "wst_gemv_hier_rmsnorm: norm weight and h must be 16-byte aligned");
   const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, bias, y, in_f, out_f, accum};
@@ -462,7 +509,7 @@ extern "C" wst_status_t wst_gemv_hier_swiglu(const void *qw, const void *si, con
                                              void *out, int32_t in_f, int32_t inter) {
   const wst_status_t st = check_common(qw, si, sb, x, out, in_f, inter, "wst_gemv_hier_swiglu");
   if (st != WST_OK) return st;
-  WST_REQUIRE(in_f <= 28672, "wst_gemv_hier_swiglu: in_features above 28672");
+  WST_REQUIRE(in_f / HGROUP <= GEMV_MAX_G, "wst_gemv_hier_swiglu: in_features above 24576");
   WST_REQUIRE(!((uintptr_t)norm_w & 15u), "wst_gemv_hier_swiglu: norm weight must be 16-byte aligned");
   const HierArgs a{qw, si, sb, x, norm_w, eps, nullptr, nullptr, out, in_f, inter, 0};
   const int ti = hier_tile_index(in_f, 2 * inter);
