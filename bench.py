@@ -1,0 +1,267 @@
+"""Batch=1 int4-hier-g32 decode benchmark on one MI355X.
+
+Workload (default, the configuration the headline metric is quoted on):
+Qwen2.5-7B-shaped decoder (28 layers, hidden 3584, 28 q / 4 kv heads of 128,
+SwiGLU 18944, vocab 152064, untied int4 lm_head), seeded synthetic weights
+packed to int4-hier-g32 on the device, KV caches filled with seeded f16 for
+positions 0..2047, then `--steps` greedy tokens (2048 -> 2304 at the default
+256), one captured-graph replay and a 4-byte token read back per token, as the
+reference's generate loop does.
+
+The line printed carries:
+  value      tok/s over the timed steps (inputs resident in HBM)
+  roofline   the dominant kernel (largest share of the step's time) timed with
+             HIP events over back-to-back launches of all its layer instances;
+             achieved = algorithmic bytes per launch / average launch time
+  kernels    the same figures for every stage kernel
+  cpu_baseline  the CPU oracle (oracle/, a C restatement of the reference's
+             dequant + forward) on the same weights and context, timed on the
+             host cores for a bounded number of tokens
+  cpu_check  the GPU's first-step logits and tokens against that CPU run
+
+    python bench.py [--steps 256] [--warmup 8] [--config 3|2] [--cpu-seconds 12]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "batch=1 decode tok/s + achieved HBM GB/s (% of 8 TB/s), Qwen2.5-0.5B/7B int4"
+HBM_PEAK_GBS = 8000.0
+KV_SEED, WEIGHT_SEED, PROMPT_SEED = 2, 0, 1
+TIMED_STAGES = ["qkv", "attn", "o", "gate_up", "down", "head"]
+KERNEL_NAMES = {  # kernel each stage launches in the fused step (rocprof names)
+    "qkv": "gemv_hier_kernel<..., NORM=true, SWIGLU=false>",
+    "attn": "attn_decode_kernel<LP, ROPE=true>",
+    "o": "gemv_hier_kernel<..., NORM=false, SWIGLU=false>",
+    "gate_up": "gemv_hier_kernel<..., NORM=true, SWIGLU=true>",
+    "down": "gemv_hier_kernel<..., NORM=false, SWIGLU=false>",
+    "head": "gemv_hier_kernel<..., NORM=true, SWIGLU=false>",
+}
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.md"
+
+
+def log(msg: str) -> None:
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=256)
+    p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--config", type=int, default=3, choices=(2, 3))
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="CPU baseline budget (tokens are added until it is spent)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--stage-reps", type=int, default=20)
+    return p.parse_args()
+
+
+def traffic_for(config: int, stage: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE,
+    scaled by the same counters' reading for a copy of known size; committed
+    in profiles/traffic.md as `traffic cfg<N> <stage>: <bytes>` lines."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    key = f"traffic cfg{config} {stage}:"
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        line = line.strip().strip("`")
+        if line.startswith(key):
+            return int(line[len(key):].strip().split()[0])
+    return None
+
+
+def copy_model_to_oracle(g, o, cfg):
+    """Device packed bytes -> the oracle's (zero-initialised) host matrices."""
+    from whetstone_amd import ffi
+    names = ["embed"] + ([] if cfg["tied"] else ["lm_head"])
+    names += [f"L{l}.{t}" for l in range(cfg["n_layers"]) for t in ("qkv", "o", "gate_up", "down")]
+    for name in names:
+        qw, si, sb, i, n = g.tensor(name)
+        p = o.tensor(name)
+        assert (p.in_f, p.out_f) == (i, n), name
+        for dst, src in ((p.qw, qw), (p.si, si), (p.sb, sb)):
+            ffi.check(ffi.lib().wst_memcpy_d2h(dst.ctypes.data, src, dst.nbytes))
+
+
+def cpu_leg(g, cfg, ctx0, first_token, gpu_tokens, gpu_logits0, budget_s, same_context):
+    """Times the oracle's precision-mirrored decode on the same weights and a
+    synthetic context of the same length; when that context is the GPU's own
+    (same_context), also checks the GPU's first logits and tokens."""
+    from oracle import oracle as O
+    t0 = time.perf_counter()
+    o = O.Model(cfg, WEIGHT_SEED, pack=False)
+    copy_model_to_oracle(g, o, cfg)
+    st = O.State(o, ctx0 + 64, 0)
+    st.fill_kv(KV_SEED, ctx0)
+    st.pos = ctx0
+    setup_s = time.perf_counter() - t0
+    tok, times, toks, lg0 = first_token, [], [], None
+    while True:
+        t = time.perf_counter()
+        nxt, lg = st.step(tok)
+        times.append(time.perf_counter() - t)
+        if lg0 is None:
+            lg0 = lg
+        toks.append(nxt)
+        tok = nxt
+        if sum(times) >= budget_s or len(times) >= 16:
+            break
+    lg_text = None
+    if same_context:  # the f64 textbook forward (no f16 narrowing) for one step
+        tb = O.State(o, ctx0 + 64, 1)
+        tb.fill_kv(KV_SEED, ctx0)
+        tb.pos = ctx0
+        _, lg_text = tb.step(first_token)
+        tb.close()
+    n = len(toks)
+    base = {
+        "value": round(n / sum(times), 4),
+        "unit": "tok/s",
+        "cores": int(O.lib().orc_threads()),
+        "kind": "port",
+        "sample": (f"{n} greedy tokens from a {ctx0}-token context on the same packed weights: "
+                   f"oracle/oracle.c precision-mirrored forward (dequant on the fly, f64 dot "
+                   f"products), OpenMP over rows; setup {setup_s:.1f}s not timed"),
+    }
+    o.close()
+    if not same_context:
+        return base, None
+    diff = np.abs(gpu_logits0.astype(np.float64) - lg0)
+    rel = diff / np.maximum(np.abs(lg0), 1.0)
+    check = {
+        "tokens_compared": n,
+        "tokens_identical": int(sum(int(a) == int(b) for a, b in zip(toks, gpu_tokens[:n]))),
+        "first_step_logits_max_abs": float(diff.max()),
+        "first_step_logits_max_rel": float(rel.max()),
+        "first_step_within_tolerance": bool(np.allclose(gpu_logits0, lg0, rtol=1e-3, atol=1e-2)),
+        "first_step_top2_margin": O.top2_margin(lg0),
+        "first_step_gpu_vs_textbook_max_abs": float(np.max(np.abs(gpu_logits0 - lg_text))),
+        "first_step_mirrored_vs_textbook_max_abs": float(np.max(np.abs(lg0 - lg_text))),
+        "first_step_logit_rms": float(np.sqrt(np.mean(lg_text.astype(np.float64) ** 2))),
+    }
+    return base, check
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
+              "(the path's sharding is described in DESIGN.md, not built)", file=sys.stderr)
+        sys.exit(2)
+    if a.steps <= 0 or a.warmup < 0:
+        sys.exit("bench.py: --steps must be positive and --warmup non-negative")
+
+    from whetstone_amd import engine as E, kernels as wk  # raises if not built
+    cfg = E.QWEN7B if a.config == 3 else E.QWEN05B
+    t_gen = time.perf_counter()
+    g = E.Model(cfg, seed=WEIGHT_SEED)
+    wk.synchronize()
+    t_gen = time.perf_counter() - t_gen
+
+    if a.config == 3:
+        ctx0 = 2048
+        eng = E.Engine(g, ctx0 + max(a.steps, a.warmup) + 8)
+        eng.fill_kv(KV_SEED, ctx0)
+        workload = ("config 3: Qwen2.5-7B-shape int4 hier-g32 batch=1 greedy decode, "
+                    f"KV context {ctx0} -> {ctx0 + a.steps}")
+    else:
+        ctx0 = 512
+        eng = E.Engine(g, ctx0 + max(a.steps, a.warmup) + 8)
+        prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], ctx0)
+        eng.prefill(prompt.astype(np.int32), chunked=True)
+        workload = ("config 2: Qwen2.5-0.5B-shape int4 hier-g32 batch=1 greedy decode after a "
+                    f"{ctx0}-token chunked prefill, context {ctx0} -> {ctx0 + a.steps}")
+    log(f"model ready ({t_gen:.2f}s), context {ctx0}; capturing the step graph")
+    eng.capture_graph()  # warm-up step + rewind inside
+    log("graph captured; warm-up")
+    tok0 = eng.token()
+    for _ in range(a.warmup):
+        eng.step()
+        eng.token()
+    eng.set_pos(ctx0)
+    eng.forward(tok0)  # the first timed step's inputs again, eagerly, for the logits check
+    logits0 = eng.logits()
+    eng.set_pos(ctx0)
+    eng.set_token(tok0)
+
+    log(f"timing {a.steps} steps")
+    bytes_steps = []
+    tokens = []
+    wk.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        eng.step()
+        tokens.append(eng.token())
+    wk.synchronize()
+    dt = time.perf_counter() - t0
+    # bytes of each timed step (position ctx0 + i reads ctx0 + i + 1 cached rows)
+    for i in range(a.steps):
+        eng.set_pos(ctx0 + i)
+        bytes_steps.append(eng.step_bytes())
+    bytes_tok = float(np.mean(bytes_steps))
+
+    log(f"{a.steps / dt:.1f} tok/s; timing each stage kernel")
+    # Per-kernel timing at the middle of the timed context range.
+    eng.set_pos(ctx0 + a.steps // 2)
+    kernels = {}
+    launches = {"head": 1}
+    for s in TIMED_STAGES:
+        us, b = eng.time_stage(s, a.stage_reps)
+        n = launches.get(s, cfg["n_layers"])
+        kernels[s] = {"kernel": KERNEL_NAMES[s], "us_per_launch": round(us, 3),
+                      "bytes_per_launch": b, "gbs": round(b / us / 1e3, 1),
+                      "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                      "launches_per_token": n, "us_per_token": round(us * n, 1)}
+    dom = max(kernels, key=lambda s: kernels[s]["us_per_token"])
+    k = kernels[dom]
+    roofline = {"bound": "hbm", "kernel": f"{dom}: {k['kernel']}", "achieved": k["gbs"],
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": k["frac"],
+                "traffic": traffic_for(a.config, dom)}
+
+    tok_s = a.steps / dt
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(dt / a.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xf16->f32",
+        "data": "synthetic (seeded N(0,0.02) weights packed to int4-hier-g32 on the device; "
+                + ("seeded f16 N(0,1) KV context)" if a.config == 3 else "seeded random prompt)"),
+        "config": {"workload": workload, "bytes_per_token": int(bytes_tok),
+                   "hbm_gbs": round(bytes_tok * tok_s / 1e9, 1),
+                   "frac_of_hbm_peak": round(bytes_tok * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+                   "token_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bytes_tok, 1),
+                   "graph": True, "weights_generated_s": round(t_gen, 2)},
+        "roofline": roofline,
+        "kernels": kernels,
+    }
+    if a.no_cpu:
+        line["cpu_baseline"] = None
+    else:
+        log("CPU baseline (oracle) on the same weights")
+        base, check = cpu_leg(g, cfg, ctx0, tok0, tokens, logits0, a.cpu_seconds,
+                              same_context=a.config == 3)
+        line["cpu_baseline"] = base
+        line["cpu_check"] = check
+    eng.close()
+    g.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -100,10 +100,22 @@ wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids_host, int32_
 wst_status_t wse_engine_generate(wse_engine_t *e, const int32_t *prompt_host, int32_t n_prompt,
                                  int32_t n_new, int32_t chunked, int32_t *out_tokens_host);
 wst_status_t wse_engine_token(wse_engine_t *e, int32_t *out);
+/* Writes `token` into the device token cursor (the next step's input). */
+wst_status_t wse_engine_set_token(wse_engine_t *e, int32_t token);
 wst_status_t wse_engine_logits(wse_engine_t *e, float *out_host);
 /* One eager step with an event at every stage boundary; adds the elapsed ms
  * per stage into stage_ms[WSE_STAGES] and launch counts into counts. */
 wst_status_t wse_engine_profile_step(wse_engine_t *e, double *stage_ms, int32_t *counts);
+/* Average duration of one launch of a stage's kernel in the fused step, timed
+ * with events on the calling thread's stream over `reps` sweeps that launch
+ * every layer's instance back to back (HEAD: the one head GEMV per sweep), and
+ * the algorithmic bytes one launch moves (packed weights, norm gains, biases,
+ * activations read and written; ATTN: the K/V rows of every cached position).
+ * Stages QKV, ATTN, O, GATE_UP, DOWN, HEAD; WSE_STEP_FUSED engines only.
+ * Activations are overwritten and the current position's K/V rewritten with
+ * the same values; the position and token cursor are unchanged. */
+wst_status_t wse_engine_time_stage(wse_engine_t *e, int32_t stage, int32_t reps,
+                                   double *us_per_launch, uint64_t *bytes_per_launch);
 /* Algorithmic bytes of one decode step at the current position. */
 uint64_t wse_engine_step_bytes(const wse_engine_t *e);
 

@@ -615,7 +615,17 @@ static uint16_t *f16_fill(size_t n, float v) {
   return p;
 }
 
+static orc_model_t *model_build(const orc_config_t *cfg, uint64_t seed, int pack);
+
 orc_model_t *orc_model_synthetic(const orc_config_t *cfg, uint64_t seed) {
+  return model_build(cfg, seed, 1);
+}
+
+orc_model_t *orc_model_alloc(const orc_config_t *cfg, uint64_t seed) {
+  return model_build(cfg, seed, 0);
+}
+
+static orc_model_t *model_build(const orc_config_t *cfg, uint64_t seed, int pack) {
   orc_model_t *m = (orc_model_t *)calloc(1, sizeof(orc_model_t));
   m->c = *cfg;
   const orc_config_t *c = cfg;
@@ -623,10 +633,10 @@ orc_model_t *orc_model_synthetic(const orc_config_t *cfg, uint64_t seed) {
   const int64_t nq = (int64_t)c->n_q * hd, nk = (int64_t)c->n_kv * hd;
 
   hmat_alloc(&m->embed, H, V);
-  pack_part(&m->embed, 0, V, seed, ST_EMBED, NULL);
+  if (pack) pack_part(&m->embed, 0, V, seed, ST_EMBED, NULL);
   if (!c->tied) {
     hmat_alloc(&m->lm_head, H, V);
-    pack_part(&m->lm_head, 0, V, seed, ST_HEAD, NULL);
+    if (pack) pack_part(&m->lm_head, 0, V, seed, ST_HEAD, NULL);
   }
   m->final_norm = f16_fill((size_t)H, 1.0f);
   if (c->rescore_k > 0) {
@@ -643,16 +653,16 @@ orc_model_t *orc_model_synthetic(const orc_config_t *cfg, uint64_t seed) {
   for (int l = 0; l < c->n_layers; ++l) {
     layer_t *L = &m->layers[l];
     hmat_alloc(&L->qkv, H, nq + 2 * nk);
-    pack_part(&L->qkv, 0, nq, seed, STREAM(l, ST_Q), NULL);
-    pack_part(&L->qkv, nq, nk, seed, STREAM(l, ST_K), NULL);
-    pack_part(&L->qkv, nq + nk, nk, seed, STREAM(l, ST_V), NULL);
+    if (pack) pack_part(&L->qkv, 0, nq, seed, STREAM(l, ST_Q), NULL);
+    if (pack) pack_part(&L->qkv, nq, nk, seed, STREAM(l, ST_K), NULL);
+    if (pack) pack_part(&L->qkv, nq + nk, nk, seed, STREAM(l, ST_V), NULL);
     hmat_alloc(&L->o, nq, H);
-    pack_part(&L->o, 0, H, seed, STREAM(l, ST_O), NULL);
+    if (pack) pack_part(&L->o, 0, H, seed, STREAM(l, ST_O), NULL);
     hmat_alloc(&L->gate_up, H, 2 * I);
-    pack_part(&L->gate_up, 0, I, seed, STREAM(l, ST_GATE), NULL);
-    pack_part(&L->gate_up, I, I, seed, STREAM(l, ST_UP), NULL);
+    if (pack) pack_part(&L->gate_up, 0, I, seed, STREAM(l, ST_GATE), NULL);
+    if (pack) pack_part(&L->gate_up, I, I, seed, STREAM(l, ST_UP), NULL);
     hmat_alloc(&L->down, I, H);
-    pack_part(&L->down, 0, H, seed, STREAM(l, ST_DOWN), NULL);
+    if (pack) pack_part(&L->down, 0, H, seed, STREAM(l, ST_DOWN), NULL);
     L->qkv_bias = c->qkv_bias ? f16_fill((size_t)(nq + 2 * nk), 0.0f) : NULL;
     L->in_norm = f16_fill((size_t)H, 1.0f);
     L->post_norm = f16_fill((size_t)H, 1.0f);

@@ -91,6 +91,10 @@ typedef struct orc_state orc_state_t;
 /* Seeded synthetic model: every Linear and the Embedding ~N(0,0.02) f32, packed
  * to hier-g32; q/k/v biases 0; norm gains 1; QK-norm gains 1+N(0,0.02). */
 orc_model_t *orc_model_synthetic(const orc_config_t *cfg, uint64_t seed);
+/* The same model with its packed matrices allocated but left zero, for a
+ * caller that copies packed bytes in through orc_model_tensor's pointers (the
+ * bench's CPU leg copies the device model's bytes). */
+orc_model_t *orc_model_alloc(const orc_config_t *cfg, uint64_t seed);
 void orc_model_free(orc_model_t *m);
 /* Raw views of the packed tensors, for tests that compare bytes.
  * name: "embed", "lm_head", "L<l>.qkv", "L<l>.o", "L<l>.gate_up", "L<l>.down". */

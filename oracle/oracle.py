@@ -81,6 +81,7 @@ def lib():
                                            C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
         "orc_head_rescore": (None, [_u16p, _u16p, _f32p, C.c_int, C.c_int, C.c_float]),
         "orc_model_synthetic": (C.c_void_p, [C.POINTER(Config), C.c_uint64]),
+        "orc_model_alloc": (C.c_void_p, [C.POINTER(Config), C.c_uint64]),
         "orc_model_free": (None, [C.c_void_p]),
         "orc_model_tensor": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p),
                                        C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
@@ -219,10 +220,13 @@ def make_config(**kw) -> Config:
 class Model:
     """A seeded synthetic model packed by the oracle's quantiser."""
 
-    def __init__(self, cfg: dict, seed: int = 0):
+    def __init__(self, cfg: dict, seed: int = 0, pack: bool = True):
+        """pack=False leaves the packed matrices zero, for a caller that copies
+        packed bytes in through tensor()'s (writable) views."""
         self.cfg = dict(cfg)
         self._c = make_config(**self.cfg)
-        self.h = lib().orc_model_synthetic(C.byref(self._c), seed)
+        make = lib().orc_model_synthetic if pack else lib().orc_model_alloc
+        self.h = make(C.byref(self._c), seed)
         self.seed = seed
 
     def close(self):

@@ -34,13 +34,17 @@
 
 #define ATTN_MAX_GQA 8
 #define ATTN_MAX_SPLITS 16
+#define ATTN_MERGE_BATCH 16  // slices fetched per round trip in the merge
 #define ATTN_UNROLL 4
 #define ATTN_WAVES 8
 #define ATTN_THREADS (64 * ATTN_WAVES)
 
 static inline int attn_splits(int n_kv, int max_seq) {
   // Slices of at least 128 cached positions, at most 16 of them (the merge
-  // fetches every slice in one batch), and no more than ~1 block per CU.
+  // then fetches every slice in one batch), and no more than about one block
+  // per CU. (Measured on the 7B shape at ctx 2048: 32 slices of 64 positions
+  // are slower -- the merge and the last-block hand-off grow with the slice
+  // count faster than the per-slice sweep shrinks.)
   // WST_ATTN_SPLITS caps the slice count (for sweeps).
   static int cap_env = -1;
   if (cap_env < 0) {
@@ -76,15 +80,16 @@ struct RopeArgs {
 
 // Sum over the LP lanes of a position (aligned groups of 8, 16 or 32 lanes),
 // returned in all of them. DPP row operations (quad swaps, half-row and row
-// mirrors): a few VALU cycles per step, where lane shuffles through LDS cost a
-// round trip each and made the score reduction the kernel's bottleneck.
+// mirrors, then the gfx950 row swap): a few VALU cycles per step, where lane
+// shuffles through LDS cost a round trip each and made the score reduction the
+// kernel's bottleneck.
 template <int LP>
 __device__ __forceinline__ float pos_group_sum(float v) {
   v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp_f<0x141>(v);  // row_half_mirror: lane i + lane 7-i of each 8
   if constexpr (LP >= 16) v += dpp_f<0x140>(v);  // row_mirror
-  if constexpr (LP >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (LP >= 32) v = xrow16_sum(v);
   return v;
 }
 
@@ -245,18 +250,39 @@ __global__ __launch_bounds__(ATTN_THREADS) void attn_decode_kernel(
     }
   }
 
-  // Merge the position groups of this wave (lanes with equal `sub`).
-#pragma unroll
-  for (int o = LP; o < 64; o <<= 1) {
+  // Merge the position groups of this wave (lanes with equal `sub`): groups
+  // 8 lanes apart by a DPP row rotation, 16 and 32 apart by the row swaps.
+  // softmax_merge is exactly commutative, so both partners end with the same
+  // bits.
+  if constexpr (LP == 8) {
 #pragma unroll
     for (int h = 0; h < MAXG; ++h) {
       if (h >= gqa) break;
-      const float mo = __shfl_xor(m[h], o, 64);
-      const float lo = __shfl_xor(l[h], o, 64);
       float ao[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ao[i] = __shfl_xor(acc[h][i], o, 64);
-      softmax_merge(m[h], l[h], acc[h], mo, lo, ao);
+      for (int i = 0; i < 8; ++i) ao[i] = dpp_f<0x128>(acc[h][i]);  // row_ror:8
+      softmax_merge(m[h], l[h], acc[h], dpp_f<0x128>(m[h]), dpp_f<0x128>(l[h]), ao);
+    }
+  }
+#pragma unroll
+  for (int o = (LP > 16 ? LP : 16); o < 64; o <<= 1) {
+#pragma unroll
+    for (int h = 0; h < MAXG; ++h) {
+      if (h >= gqa) break;
+      const RowPair pm = o == 16 ? xrow16(m[h]) : xrow32(m[h]);
+      const RowPair pl = o == 16 ? xrow16(l[h]) : xrow32(l[h]);
+      float aa[8], ab[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const RowPair pa = o == 16 ? xrow16(acc[h][i]) : xrow32(acc[h][i]);
+        aa[i] = pa.a;
+        ab[i] = pa.b;
+      }
+      m[h] = pm.a;
+      l[h] = pl.a;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[h][i] = aa[i];
+      softmax_merge(m[h], l[h], acc[h], pm.b, pl.b, ab);
     }
   }
 
@@ -304,36 +330,48 @@ __global__ __launch_bounds__(ATTN_THREADS) void attn_decode_kernel(
   if (!last_block_done(counters + kvh, (unsigned int)splits)) return;
 
   // Slice merge for the gqa heads of this kv head (attention.cu:170-193): one
-  // thread per (head, 4 dims) fetches all slices' (m, l) and numerators in one
-  // batch, then combines them in slice order.
+  // thread per (head, 4 dims) fetches the slices' (m, l) and numerators in
+  // batches of ATTN_MERGE_BATCH (one round trip each) and combines them in
+  // slice order, rescaling the running sum when a batch raises the maximum.
   for (int k = tid; k < gqa * (HD / 4); k += ATTN_THREADS) {
     const int h = k / (HD / 4), d4 = k % (HD / 4);
     const size_t row0 = (size_t)(kvh * gqa + h) * splits;
-    float ms[ATTN_MAX_SPLITS], ls[ATTN_MAX_SPLITS];
-    float4 vs[ATTN_MAX_SPLITS];
-#pragma unroll
-    for (int s = 0; s < ATTN_MAX_SPLITS; ++s) {
-      if (s < splits) {
-        ms[s] = pml[(row0 + s) * 2];
-        ls[s] = pml[(row0 + s) * 2 + 1];
-        vs[s] = ((const float4 *)(pacc + (row0 + s) * HD))[d4];
-      }
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
-      if (s < splits) M = fmaxf(M, ms[s]);
+    float M = -INFINITY, den = 0.0f;
     float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float den = 0.0f;
+    for (int c0 = 0; c0 < splits; c0 += ATTN_MERGE_BATCH) {
+      float ms[ATTN_MERGE_BATCH], ls[ATTN_MERGE_BATCH];
+      float4 vs[ATTN_MERGE_BATCH];
+      // Unconditional loads (a clamped slice index) so that all of them are
+      // in flight together; guarded loads compile to one round trip each.
 #pragma unroll
-    for (int s = 0; s < ATTN_MAX_SPLITS; ++s) {
-      if (s >= splits) break;
-      const float f = (ms[s] == -INFINITY) ? 0.0f : __expf(ms[s] - M);
-      a.x = fmaf(vs[s].x, f, a.x);
-      a.y = fmaf(vs[s].y, f, a.y);
-      a.z = fmaf(vs[s].z, f, a.z);
-      a.w = fmaf(vs[s].w, f, a.w);
-      den = fmaf(ls[s], f, den);
+      for (int i = 0; i < ATTN_MERGE_BATCH; ++i) {
+        const int s = c0 + i;
+        const size_t r = row0 + (s < splits ? s : splits - 1);
+        const float2 ml = *(const float2 *)(pml + r * 2);
+        ms[i] = s < splits ? ml.x : -INFINITY;
+        ls[i] = ml.y;
+        vs[i] = ((const float4 *)(pacc + r * HD))[d4];
+      }
+      float Mn = M;
+#pragma unroll
+      for (int i = 0; i < ATTN_MERGE_BATCH; ++i) Mn = fmaxf(Mn, ms[i]);
+      const float fo = (M == -INFINITY) ? 0.0f : __expf(M - Mn);
+      a.x *= fo;
+      a.y *= fo;
+      a.z *= fo;
+      a.w *= fo;
+      den *= fo;
+#pragma unroll
+      for (int i = 0; i < ATTN_MERGE_BATCH; ++i) {
+        if (c0 + i >= splits) break;  // uniform; loads are already done
+        const float f = (ms[i] == -INFINITY) ? 0.0f : __expf(ms[i] - Mn);
+        a.x = fmaf(vs[i].x, f, a.x);
+        a.y = fmaf(vs[i].y, f, a.y);
+        a.z = fmaf(vs[i].z, f, a.z);
+        a.w = fmaf(vs[i].w, f, a.w);
+        den = fmaf(ls[i], f, den);
+      }
+      M = Mn;
     }
     uint16_t *o = out + (size_t)(kvh * gqa + h) * HD + d4 * 4;
     o[0] = f2h(a.x / den);

@@ -129,42 +129,96 @@ __device__ __forceinline__ float dpp_max16(float v) {
   return v;
 }
 
-// Sum over the 32 lanes of each half wave, returned in every lane of that half.
-__device__ __forceinline__ float half_wave_sum(float v) {
-  v = dpp_sum16(v);
-  // Combine rows 0+1 and 2+3: every lane adds the value of lane ^ 16.
-  v += __shfl_xor(v, 16, 64);
-  return v;
+// Cross-row exchange (gfx950 v_permlane16_swap / v_permlane32_swap, plain
+// VALU ops). permlane16_swap(a, b) swaps the odd 16-lane rows of a with the
+// even rows of b; called with a == b == v it returns, in both lanes of every
+// pair (i, i^16), the even row's value in one result and the odd row's in the
+// other (permlane32_swap: the same for the two 32-lane halves). Every caller
+// combines the two with a commutative operation, so both lanes of a pair
+// compute the same bits whichever result holds which row.
+struct RowPair {
+  float a, b;
+};
+__device__ __forceinline__ RowPair xrow16(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return {__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
 }
+__device__ __forceinline__ RowPair xrow32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return {__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+__device__ __forceinline__ float xrow16_sum(float v) {
+  const RowPair p = xrow16(v);
+  return p.a + p.b;
+}
+__device__ __forceinline__ float xrow32_sum(float v) {
+  const RowPair p = xrow32(v);
+  return p.a + p.b;
+}
+
+// Sum over the 32 lanes of each half wave, returned in every lane of that half.
+__device__ __forceinline__ float half_wave_sum(float v) { return xrow16_sum(dpp_sum16(v)); }
 
 // Sum over the whole wave, in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
-  v = dpp_sum16(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  return xrow32_sum(xrow16_sum(dpp_sum16(v)));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
   v = dpp_max16(v);
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
+  RowPair p = xrow16(v);
+  v = fmaxf(p.a, p.b);
+  p = xrow32(v);
+  return fmaxf(p.a, p.b);
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
 
 __device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_i<0xB1>(v);
+  v += dpp_i<0x4E>(v);
+  v += dpp_i<0x141>(v);
+  v += dpp_i<0x140>(v);
+  uint32_t u = (uint32_t)v;
+  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  u = (uint32_t)r[0] + (uint32_t)r[1];
+  r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return (int)((uint32_t)r[0] + (uint32_t)r[1]);
 }
 
+__device__ __forceinline__ unsigned long long u64_max(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+  const int lo = dpp_i<CTRL>((int)(uint32_t)v), hi = dpp_i<CTRL>((int)(uint32_t)(v >> 32));
+  return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+__device__ __forceinline__ unsigned long long xrow_u64_max(unsigned long long v, bool x32) {
+  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  const auto rl = x32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                      : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto rh = x32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                      : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  return u64_max(((unsigned long long)(uint32_t)rh[0] << 32) | (uint32_t)rl[0],
+                 ((unsigned long long)(uint32_t)rh[1] << 32) | (uint32_t)rl[1]);
+}
+
+// Maximum over the wave. Within a 16-lane row the quad swaps and mirrors pair
+// every lane with one of the other group at each step (a maximum does not
+// need the xor pairing a lane-wise sum of vectors would).
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long t = __shfl_xor(v, o, 64);
-    v = t > v ? t : v;
-  }
-  return v;
+  v = u64_max(v, dpp_u64<0xB1>(v));
+  v = u64_max(v, dpp_u64<0x4E>(v));
+  v = u64_max(v, dpp_u64<0x141>(v));
+  v = u64_max(v, dpp_u64<0x140>(v));
+  v = xrow_u64_max(v, false);
+  return xrow_u64_max(v, true);
 }
 
 // Block-wide sum for blocks of up to 1024 threads; every thread gets the
@@ -248,20 +302,27 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
 // "Last block done": every block calls this once after publishing its partial
 // result with plain stores. The block that observes count == nblocks-1 returns
 // true (in every thread) and owns the final combine; it also resets the
-// counter to zero so the next launch (or a graph replay) starts clean. Device
-// scope release/acquire fences make the other blocks' stores visible across
-// XCDs.
+// counter to zero so the next launch (or a graph replay) starts clean.
+//
+// Visibility: every wave waits for its own stores to complete (s_waitcnt 0;
+// a workgroup barrier alone does not wait for global stores), then the
+// barrier orders them before thread 0's
+// agent-scope acq_rel add (on gfx950 an L2 write-back, the atomic, then an
+// L1/L2 invalidate of this CU and XCD), which makes them visible across XCDs
+// and, in the last block, invalidates stale lines before the second barrier
+// releases the other waves to read. Agent scope only: a system-scope fence
+// writes back and invalidates for the host as well, which cost several
+// microseconds per launch.
 __device__ __forceinline__ bool last_block_done(unsigned int *counter, unsigned int nblocks) {
   __shared__ bool is_last;
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    __atomic_thread_fence(__ATOMIC_RELEASE);
     const unsigned int prev =
         __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     is_last = (prev == nblocks - 1);
     if (is_last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  if (is_last) __atomic_thread_fence(__ATOMIC_ACQUIRE);
   return is_last;
 }

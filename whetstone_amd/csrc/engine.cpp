@@ -518,9 +518,88 @@ wst_status_t wse_engine_profile_step(wse_engine_t *e, double *stage_ms, int32_t 
   return WST_OK;
 }
 
+// One launch of `stage`'s fused kernel for layer l (the same call step_eager
+// makes), and its algorithmic bytes.
+static wst_status_t stage_launch(wse_engine *e, int stage, int l, uint64_t *bytes) {
+  const wse_model &m = *e->m;
+  const wse_config_t &c = m.c;
+  const int H = c.hidden, hd = c.head_dim, nq = c.n_q, nkv = c.n_kv, I = c.inter, V = c.vocab;
+  const int nqkv = (nq + 2 * nkv) * hd;
+  const float eps = c.eps;
+  const Layer &L = m.layers[(size_t)l];
+  const uint64_t seq = (uint64_t)(e->pos + 1 < e->max_seq ? e->pos + 1 : e->max_seq);
+  switch (stage) {
+    case WSE_STAGE_QKV:
+      *bytes = L.qkv.bytes() + (uint64_t)H * 6 + (L.qkv_bias ? (uint64_t)nqkv * 2 : 0) +
+               (uint64_t)nqkv * 4;
+      return wst_gemv_hier_rmsnorm(L.qkv.qw, L.qkv.si, L.qkv.sb, e->x, L.in_norm, eps, nullptr,
+                                   L.qkv_bias, e->qkv, H, nqkv, 0);
+    case WSE_STAGE_ATTN:
+      *bytes = 2 * (uint64_t)nkv * seq * (uint64_t)hd * 2 + (uint64_t)nqkv * 4 + (uint64_t)nq * hd * 2;
+      return wst_attn_decode_fused(e->qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab,
+                                   e->sin_tab, e->partials, e->attn, nq, nkv, hd, e->pos_dev,
+                                   e->max_seq, (float)(1.0 / sqrt((double)hd)), L.q_norm,
+                                   L.k_norm, eps);
+    case WSE_STAGE_O:
+      *bytes = L.o.bytes() + (uint64_t)nq * hd * 2 + (uint64_t)H * 8;
+      return wst_gemv_int4_hier_ex(L.o.qw, L.o.si, L.o.sb, e->attn, nullptr, e->x, nq * hd, H, 1);
+    case WSE_STAGE_GATE_UP:
+      *bytes = L.gate_up.bytes() + (uint64_t)H * 6 + (uint64_t)I * 2;
+      return wst_gemv_hier_swiglu(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->x, L.post_norm,
+                                  eps, e->act, H, I);
+    case WSE_STAGE_DOWN:
+      *bytes = L.down.bytes() + (uint64_t)I * 2 + (uint64_t)H * 8;
+      return wst_gemv_int4_hier_ex(L.down.qw, L.down.si, L.down.sb, e->act, nullptr, e->x, I, H,
+                                   1);
+    case WSE_STAGE_HEAD: {
+      const Mat &head = m.head();
+      *bytes = head.bytes() + (uint64_t)H * 8 + (uint64_t)V * 4;
+      return wst_gemv_hier_rmsnorm(head.qw, head.si, head.sb, e->x, m.final_norm, eps, e->h,
+                                   nullptr, e->logits, H, V, 0);
+    }
+    default:
+      snprintf(g_msg, sizeof(g_msg), "stage %d cannot be timed on its own", stage);
+      return WST_ERR_INVALID_ARG;
+  }
+}
+
+wst_status_t wse_engine_time_stage(wse_engine_t *e, int32_t stage, int32_t reps,
+                                   double *us_per_launch, uint64_t *bytes_per_launch) {
+  if (!e || !us_per_launch || reps <= 0) return WST_ERR_INVALID_ARG;
+  if (e->mode != WSE_STEP_FUSED) {
+    snprintf(g_msg, sizeof(g_msg), "stage timing needs a WSE_STEP_FUSED engine");
+    return WST_ERR_INVALID_ARG;
+  }
+  const int per = stage == WSE_STAGE_HEAD ? 1 : e->m->c.n_layers;
+  uint64_t bytes = 0, total = 0;
+  for (int l = 0; l < per; ++l) {  // warm-up sweep
+    TRY(stage_launch(e, stage, l, &bytes));
+    total += bytes;
+  }
+  while (e->events.size() < 2) {
+    void *ev = nullptr;
+    TRY(wst_event_create(&ev));
+    e->events.push_back(ev);
+  }
+  TRY(wst_event_record(e->events[0]));
+  for (int r = 0; r < reps; ++r)
+    for (int l = 0; l < per; ++l) TRY(stage_launch(e, stage, l, &bytes));
+  TRY(wst_event_record(e->events[1]));
+  float ms = 0.0f;
+  TRY(wst_event_elapsed_ms(e->events[0], e->events[1], &ms));
+  *us_per_launch = (double)ms * 1e3 / ((double)reps * per);
+  if (bytes_per_launch) *bytes_per_launch = total / (uint64_t)per;
+  return WST_OK;
+}
+
 wst_status_t wse_engine_token(wse_engine_t *e, int32_t *out) {
   if (!e || !out) return WST_ERR_INVALID_ARG;
   return wst_memcpy_d2h(out, e->token, 4);
+}
+
+wst_status_t wse_engine_set_token(wse_engine_t *e, int32_t token) {
+  if (!e) return WST_ERR_INVALID_ARG;
+  return wst_memcpy_h2d(e->token, &token, 4);
 }
 
 wst_status_t wse_engine_logits(wse_engine_t *e, float *out) {

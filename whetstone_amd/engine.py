@@ -58,9 +58,11 @@ _SIG = {
     "wse_engine_prefill": (I32, [P, P, I32, I32]),
     "wse_engine_generate": (I32, [P, P, I32, I32, I32, P]),
     "wse_engine_token": (I32, [P, C.POINTER(I32)]),
+    "wse_engine_set_token": (I32, [P, I32]),
     "wse_engine_logits": (I32, [P, P]),
     "wse_engine_profile_step": (I32, [P, C.POINTER(C.c_double), C.POINTER(I32)]),
     "wse_engine_step_bytes": (C.c_uint64, [P]),
+    "wse_engine_time_stage": (I32, [P, I32, I32, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
 }
 _lib = None
 
@@ -174,6 +176,9 @@ class Engine:
                                          out.ctypes.data))
         return out[:n_new]
 
+    def set_token(self, token: int):
+        _check(lib().wse_engine_set_token(self.h, token))
+
     def token(self) -> int:
         t = C.c_int32()
         _check(lib().wse_engine_token(self.h, C.byref(t)))
@@ -191,6 +196,13 @@ class Engine:
             self.h, acc.ctypes.data_as(C.POINTER(C.c_double)),
             counts.ctypes.data_as(C.POINTER(C.c_int32))))
         return acc, counts
+
+    def time_stage(self, stage: str, reps: int = 20):
+        """(µs per launch, algorithmic bytes per launch) of one stage's kernel."""
+        us, b = C.c_double(), C.c_uint64()
+        _check(lib().wse_engine_time_stage(self.h, STAGES.index(stage), reps, C.byref(us),
+                                           C.byref(b)))
+        return us.value, int(b.value)
 
     def step_bytes(self) -> int:
         return int(lib().wse_engine_step_bytes(self.h))
