@@ -62,7 +62,73 @@ def parse():
                    help="CPU baseline budget (tokens are added until it is spent)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--stage-reps", type=int, default=20)
+    p.add_argument("--summarize", nargs="+", metavar="DIR",
+                   help="print a text summary of rocprofv3 CSV output directories "
+                        "(kernel stats, or FETCH_SIZE/WRITE_SIZE counters scaled by a "
+                        "--copy-probe run given with --calibration) and exit")
+    p.add_argument("--calibration", nargs="*", default=[], metavar="DIR",
+                   help="rocprofv3 counter directories of a --copy-probe run (its size in "
+                        "MiB by --copy-probe, default 256)")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                   help="only run the counter calibration: a device-to-device copy, a "
+                        "memset and a read sweep of MIB MiB each, then exit")
     return p.parse_args()
+
+
+def _short(name: str) -> str:
+    name = name.replace("HIP_vector_type<unsigned int, 4u>", "uint4")
+    return name.split("(")[0].replace("void ", "")[:60]
+
+
+def summarize(dirs, calibration, copy_mib) -> None:
+    """Text summary of rocprofv3 --output-format csv directories."""
+    import csv
+    import glob
+    from collections import defaultdict
+    scale = {}
+    for d in calibration:  # counter value of the copy kernel vs its known bytes
+        for f in glob.glob(os.path.join(d, "*counter_collection.csv")):
+            for r in csv.DictReader(open(f)):
+                if "copyBuffer" in r["Kernel_Name"]:  # reads and writes copy_mib MiB
+                    scale[r["Counter_Name"]] = copy_mib * 1024 / float(r["Counter_Value"])
+    for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "*kernel_stats.csv"))):
+            rows = list(csv.DictReader(open(f)))
+            print(f"kernel stats ({os.path.basename(f)}): name | calls | avg us | total ms | %")
+            for r in rows[:16]:
+                print(f"  {_short(r['Name']):60s} | {int(r['Calls']):6d} | "
+                      f"{float(r['AverageNs']) / 1e3:9.2f} | {float(r['TotalDurationNs']) / 1e6:9.2f}"
+                      f" | {float(r['Percentage']):5.1f}")
+        for f in sorted(glob.glob(os.path.join(d, "*counter_collection.csv"))):
+            agg = defaultdict(list)
+            for r in csv.DictReader(open(f)):
+                agg[(r["Counter_Name"], _short(r["Kernel_Name"]), int(r["Grid_Size"]))].append(
+                    float(r["Counter_Value"]))
+            print(f"counters ({os.path.basename(f)}): counter | kernel | grid | dispatches | "
+                  f"avg KiB/dispatch | scale | avg bytes/dispatch")
+            for (cn, kn, grid), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:16]:
+                sc = scale.get(cn, 1.0)
+                avg = sum(v) / len(v)
+                print(f"  {cn} | {kn:60s} | {grid:8d} | {len(v):5d} | {avg:12.1f} | {sc:.4f} | "
+                      f"{avg * 1024 * sc:14.0f}")
+    for cn, sc in sorted(scale.items()):
+        print(f"calibration: {cn} reads {1 / sc:.5f} KiB per KiB a copy kernel moves (scale {sc:.5f})")
+
+
+def copy_probe(mib: int) -> None:
+    """Kernels of known traffic, for scaling rocprofv3's FETCH_SIZE and
+    WRITE_SIZE readings: a copy reads and writes `mib` MiB, a memset writes
+    it, the bandwidth sweep reads it."""
+    from whetstone_amd import kernels as wk, ffi
+    n = mib << 20
+    a = wk.DeviceBuffer(n, np.uint8)
+    b = wk.DeviceBuffer(n, np.uint8)
+    for _ in range(3):
+        ffi.call("wst_memcpy_d2d", b.ptr, a.ptr, n)
+        ffi.call("wst_memset", a.ptr, 1, n)
+    gbs = wk.bench_bandwidth(n, 3)
+    wk.synchronize()
+    print(json.dumps({"copy_probe_bytes": n, "bandwidth_sweep_gbs": round(gbs, 1)}), flush=True)
 
 
 def traffic_for(config: int, stage: str):
@@ -157,6 +223,12 @@ def main():
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
               "(the path's sharding is described in DESIGN.md, not built)", file=sys.stderr)
         sys.exit(2)
+    if a.summarize:
+        summarize(a.summarize, a.calibration, a.copy_probe or 256)
+        return
+    if a.copy_probe:
+        copy_probe(a.copy_probe)
+        return
     if a.steps <= 0 or a.warmup < 0:
         sys.exit("bench.py: --steps must be positive and --warmup non-negative")
 
