@@ -188,6 +188,7 @@ def cpu_leg(g, cfg, ctx0, first_token, gpu_tokens, gpu_logits0, budget_s, same_c
         tb.pos = ctx0
         _, lg_text = tb.step(first_token)
         tb.close()
+    st.close()
     n = len(toks)
     base = {
         "value": round(n / sum(times), 4),

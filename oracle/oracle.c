@@ -760,6 +760,7 @@ const uint16_t *orc_model_fp16(orc_model_t *m, const char *name, int64_t *n) {
 struct orc_state {
   const orc_model_t *m;
   int max_seq, mode, pos;
+  int n_layers; /* kept so the state can be freed after its model */
   uint16_t **kc, **vc;  /* mode 0: f16 caches per layer */
   double **kd, **vd;    /* mode 1: f64 caches per layer */
   float *cos_tab, *sin_tab;
@@ -770,6 +771,7 @@ orc_state_t *orc_state_new(const orc_model_t *m, int max_seq, int mode) {
   s->m = m;
   s->max_seq = max_seq;
   s->mode = mode;
+  s->n_layers = m->c.n_layers;
   const orc_config_t *c = &m->c;
   const size_t n = (size_t)c->n_kv * max_seq * c->head_dim;
   if (mode == 0) {
@@ -796,7 +798,7 @@ orc_state_t *orc_state_new(const orc_model_t *m, int max_seq, int mode) {
 
 void orc_state_free(orc_state_t *s) {
   if (!s) return;
-  for (int l = 0; l < s->m->c.n_layers; ++l) {
+  for (int l = 0; l < s->n_layers; ++l) {
     if (s->kc) { free(s->kc[l]); free(s->vc[l]); }
     if (s->kd) { free(s->kd[l]); free(s->vd[l]); }
   }
