@@ -247,16 +247,18 @@ __device__ __forceinline__ float block_max(float v, float *red) {
   return s;
 }
 
-// ------------------------------------------------------------- RMS scale
-//
-// 1/sqrt(mean(x^2) + eps) over n f32 values, for a 256-thread block: thread t
-// accumulates x[t], x[t+256], ... with fmaf, then block_sum. Every kernel that
-// normalises (the RMSNorm kernel and the GEMV prologues) calls this with 256
-// threads, so they all produce the same bits.
-__device__ __forceinline__ float rms_scale256(const float *__restrict__ x, int n, float eps,
+// The RMS scale 1/sqrt(mean(x^2) + eps) of x[0..n), for 512-thread blocks:
+// thread t accumulates the 8-element blocks t, t+512, ... (each in element
+// order) with fmaf, then block_sum adds the threads in a fixed order. The
+// RMSNorm kernel and the GEMV's fused RMSNorm prologue both use this order, so
+// they produce the same f16 vector.
+__device__ __forceinline__ float rms_scale512(const float *__restrict__ x, int n, float eps,
                                               float *red) {
   float acc = 0.0f;
-  for (int i = threadIdx.x; i < n; i += 256) acc = fmaf(x[i], x[i], acc);
+  for (int b = threadIdx.x; 8 * b < n; b += 512)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (8 * b + e < n) acc = fmaf(x[8 * b + e], x[8 * b + e], acc);
   acc = block_sum(acc, red);
   return 1.0f / sqrtf(acc / (float)n + eps);
 }

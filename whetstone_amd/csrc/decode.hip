@@ -8,25 +8,25 @@
 
 // ------------------------------------------------------------------ RMSNorm
 
-// One 256-thread block per row. The scale comes from rms_scale256, the same
+// One 512-thread block per row. The scale comes from rms_scale512, the same
 // reduction the GEMV's fused RMSNorm prologue uses, so the two produce
 // identical f16 vectors.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x,
+__global__ __launch_bounds__(512) void rmsnorm_kernel(const float *__restrict__ x,
                                                       const uint16_t *__restrict__ w,
                                                       uint16_t *__restrict__ out, int n,
                                                       float eps) {
   __shared__ float red[16];
   const float *xr = x + (size_t)blockIdx.x * n;
   uint16_t *orow = out + (size_t)blockIdx.x * n;
-  const float s = rms_scale256(xr, n, eps, red);
-  for (int i = threadIdx.x; i < n; i += 256) orow[i] = f2h(xr[i] * s * h2f(w[i]));
+  const float s = rms_scale512(xr, n, eps, red);
+  for (int i = threadIdx.x; i < n; i += 512) orow[i] = f2h(xr[i] * s * h2f(w[i]));
 }
 
 extern "C" wst_status_t wst_rmsnorm(const void *x, const void *w, void *out, int32_t n,
                                     float eps) {
   WST_REQUIRE(x && w && out, "wst_rmsnorm: null pointer");
   WST_REQUIRE(n > 0, "wst_rmsnorm: n must be positive");
-  rmsnorm_kernel<<<1, 256, 0, WST_STREAM>>>((const float *)x, (const uint16_t *)w,
+  rmsnorm_kernel<<<1, 512, 0, WST_STREAM>>>((const float *)x, (const uint16_t *)w,
                                             (uint16_t *)out, n, eps);
   WST_TRY_KERNEL("wst_rmsnorm");
   return WST_OK;
@@ -38,7 +38,7 @@ extern "C" wst_status_t wst_rmsnorm_chunk(const void *x, const void *w, void *ou
                                           int32_t n, float eps) {
   WST_REQUIRE(x && w && out, "wst_rmsnorm_chunk: null pointer");
   WST_REQUIRE(dim > 0 && n > 0, "wst_rmsnorm_chunk: bad shape");
-  rmsnorm_kernel<<<n, 256, 0, WST_STREAM>>>((const float *)x, (const uint16_t *)w,
+  rmsnorm_kernel<<<n, 512, 0, WST_STREAM>>>((const float *)x, (const uint16_t *)w,
                                             (uint16_t *)out, dim, eps);
   WST_TRY_KERNEL("wst_rmsnorm_chunk");
   return WST_OK;

@@ -10,30 +10,29 @@
 // How it maps onto CDNA4
 // ----------------------
 // * One lane owns whole groups: a group is 16 bytes of nibbles, exactly one
-//   dwordx4 load, and a row-slot of 64 consecutive lanes (32 when a row has at
-//   most 32 groups) reads a contiguous run of the row. A wave therefore issues
-//   1 KB-wide coalesced loads. Waves are independent (no barriers after the
-//   prologue) and the kernel is kept near 64 VGPRs so 8 waves share a SIMD:
-//   at this size occupancy, not per-wave prefetch depth, is what keeps enough
-//   bytes in flight to stream HBM3E (measured: 5.9 TB/s of 8 on the 7B
-//   gate|up shape with this arithmetic, vs 4 TB/s at 100+ VGPRs).
-// * x lives in LDS as a per-group table prepared once per block: the 32
-//   activations of a group, permuted so that the nibble pairs produced by one
-//   bit-field insert line up with the activation pairs they multiply, plus the
-//   group's two correction sums. Entries are 80 bytes apart, which keeps a
-//   wave's ds_read_b128 free of bank conflicts.
-// * Unpack without conversions: inserting a nibble into the mantissa of f16
-//   1024.0 gives 1024+q exactly; nibbles in bits 4..7 give 1024+16q. One
-//   v_bfi_b32 per pair of weights, one shift per word, and v_dot2c_f32_f16
-//   multiplies two of them by two activations with an f32 accumulator:
-//       sum_i q_i x_i = DA + DB/16 - (1024*sum_even x + 64*sum_odd x)
-//   where DA (DB) accumulates the even (odd) columns. About 1.1 VALU
-//   instructions per weight, every product accumulated in f32 -- more precise
-//   than the reference's f16 half2 accumulation inside a group.
+//   dwordx4 load, and a row's 64 (or 64*WPR) lanes read a contiguous run of it,
+//   so a wave issues 1 KB-wide coalesced loads.
+// * The arithmetic is integer. Counted with rocprofv3 (SQ_INSTS_VALU) the
+//   earlier f16 formulation (nibble inserted into the mantissa of 1024.0, then
+//   v_dot2c_f32_f16) cost ~277 VALU instructions per row pair per lane-group on
+//   the 7B gate|up shape, about 9.5 us of SIMD time per 17 us launch: VALU was
+//   a co-bottleneck with HBM. Here each group of activations is held as a
+//   14-bit fixed-point integer split into four signed base-16 digits, and the
+//   packed nibbles feed v_dot8_i32_i4 directly: one xor and four dot8 per 8
+//   weights, no unpacking (see the activation table below).
+// * x lives in LDS as that per-group table, built once per block from the
+//   thread's own 8-column blocks while the block's first weight loads are in
+//   flight (activation loads are issued first; a wave's loads return in
+//   order). Entries are 80 bytes apart.
+// * The grid is persistent and balanced: every row slot gets the same number
+//   of rows, so no tail round runs on a fraction of the waves.
 // * Per row: y = d * sum_g ls_g*Q_g - dmin * sum_g lm_g*S_g, reduced across the
-//   row-slot with DPP. A row's value depends only on (in_f, the row's bytes,
-//   x): not on TILE, the grid, or which fused form ran, so the fused kernels
-//   can be checked bit for bit against the unfused ABI sequence.
+//   row's lanes with DPP (and LDS when a row spans waves). A row's value
+//   depends only on (in_f, the row's bytes, x): not on the grid or on which
+//   fused form ran, so the fused kernels are checked bit for bit against the
+//   unfused ABI sequence.
+// * Rows wider than GEMV_MAX_G groups fall back to a simple kernel with the f16
+//   formulation (x read from L2).
 #include "common.hpp"
 
 #include <stdlib.h>
@@ -42,7 +41,6 @@
 #define HIER_MAGIC 0x64006400u  // f16 1024.0 in both halves
 #define GEMV_THREADS 512
 #define XG_WORDS 20      // LDS words per group entry (18 used)
-#define GEMV_MAX_G 768   // groups per row handled by the LDS-table kernel
 
 // Bit-field insert (a & m) | (b & ~m) as one v_bfi_b32: the mask lives in a
 // VGPR and the magic constant in an SGPR kernel argument. (Left to itself the
@@ -124,167 +122,290 @@ __device__ __forceinline__ float slot_sum(float v) {
 
 // ---------------------------------------------------------------- the kernel
 //
-// LPR (32 or 64) lanes own a row; lane lr holds groups lr, lr+LPR, ... (NG of
-// them). A unit is TILE rows per row-slot; units are handed to waves
-// round-robin over the whole grid, so after the prologue every wave runs on
-// its own.
+// The activation table. For each group of 32 columns the block holds, in LDS:
+//   L[k][j]  k = 0..3 (8 columns each), j = 0..3: digit j of X_c for the 8
+//            columns c = 8k..8k+7, nibble i <-> column 8k+i (the packed
+//            weights' own nibble order), as signed 4-bit values in [-8, 7]
+//   C8       8 * sum_c X_c
+//   S        sum_c h_c (f32)
+//   sc       2^(e-28), e = f16 exponent field of max_c |h_c| (at least 1)
+// where X_c = rint(h_c / sc) is h in units of sc: |X_c| < 2^14, so X is h to
+// 14 bits of the group's largest value (f16 itself carries 11), exactly for
+// every h_c within 4 binades of that maximum. X_c = sum_j 16^j D_j with
+// balanced digits D_j in [-8, 7]; D_j is hex digit j of X_c + 0x8888, minus 8.
 //
-// NORM:   x is the f32 residual stream; the prologue computes the RMS scale
-//         (the same reduction as the RMSNorm kernel) and normalises with
-//         norm_w while building the table (wst_rmsnorm + GEMV). Block 0 also
-//         stores h when h_out is non-null.
-// SWIGLU: out_f is the intermediate width; unit row r computes gate row r and
-//         up row r + out_f of the fused matrix and writes f16(silu(g) * u)
-//         (GEMV + wst_swiglu).
-template <int LPR, int NG, int TILE, bool NORM, bool SWIGLU>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_hier_kernel(
+// One packed word w (8 nibbles q) against digit word j gives, in one
+// v_dot8_i32_i4 on (w xor 0x88888888) = (q - 8 per nibble),
+//     sum_i (q_i - 8) D_j,i
+// and sum_i q_i X_i = sum_j 16^j (that) + 8 sum_i X_i, all exact in int32.
+// A group then contributes  ls * sc * (sum q X)  to the row's d-term and
+// lm * S to its dmin-term:  y = d * sum_g ls_g Q_g - dmin * sum_g lm_g S_g.
+// Per 8 weights: one xor and four dot8 (the f16 route needs nine VALU ops).
+//
+// The table is built from the f16 vector the GEMV multiplies: h itself for the
+// plain form, f16(x * rms * w) for the NORM form (the same bits wst_rmsnorm
+// writes), so every form of a row computes the same value.
+#define XQ_WORDS 20  // 16 digit words + C8, S, sc, pad
+#define NORM_THREADS 512
+
+__device__ __forceinline__ int sdot8(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot8((int)a, (int)b, c, false);
+}
+// First link of a dot chain: the three-operand form with an inline zero, so no
+// accumulator is cleared by a separate move.
+__device__ __forceinline__ int sdot8z(uint32_t a, uint32_t b) {
+  int r;
+  asm("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// Table entry for one quarter (8 columns, words k = b & 3) of group b >> 2.
+// The four quarters of a group are four adjacent lanes: quad DPP ops combine
+// them, so all lanes of a quad must call this together (valid or not).
+__device__ __forceinline__ void build_xq(const uint16_t h[8], int b, bool valid,
+                                         uint32_t *__restrict__ xgt) {
+  uint32_t mx = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) mx = max(mx, (uint32_t)(h[e] & 0x7FFFu));
+  mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0xB1, 0xF, 0xF, false));
+  mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4E, 0xF, 0xF, false));
+  int ef = (int)(mx >> 10);
+  ef = ef < 1 ? 1 : (ef > 30 ? 30 : ef);
+  const float inv = __builtin_bit_cast(float, (uint32_t)(127 + 28 - ef) << 23);
+  const float sc = __builtin_bit_cast(float, (uint32_t)(127 - 28 + ef) << 23);
+  uint32_t L[4] = {0, 0, 0, 0};
+  int sx = 0;
+  float sh = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float hv = h2f(h[e]);
+    sh += hv;
+    const int X = (int)__builtin_rintf(hv * inv);
+    sx += X;
+    const uint32_t U = (uint32_t)(X + 0x8888);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) L[j] |= __builtin_amdgcn_ubfe(U, 4 * j, 4) << (4 * e);
+  }
+  sx += __builtin_amdgcn_update_dpp(0, sx, 0xB1, 0xF, 0xF, false);
+  sx += __builtin_amdgcn_update_dpp(0, sx, 0x4E, 0xF, 0xF, false);
+  sh += dpp_f<0xB1>(sh);
+  sh += dpp_f<0x4E>(sh);
+  if (valid) {
+    uint32_t *e = xgt + (size_t)(b >> 2) * XQ_WORDS;
+    const int k = b & 3;
+    *(uint4 *)(e + 4 * k) = make_uint4(L[0] ^ 0x88888888u, L[1] ^ 0x88888888u,
+                                       L[2] ^ 0x88888888u, L[3] ^ 0x88888888u);
+    if (k == 0) {
+      e[16] = (uint32_t)(8 * sx);
+      e[17] = __float_as_uint(sh);
+      e[18] = __float_as_uint(sc);
+    }
+  }
+}
+
+// y for one or two rows (SWIGLU: gate row r and up row r + nunits).
+//
+// NG groups per lane, WPR waves per row (a row's lanes are lr = 0..64*WPR-1,
+// lane lr holding groups lr, lr + 64*WPR, ...), XB activation blocks of 8 per
+// thread (in_f <= XB * 8 * NT), NT threads per block. A block works on
+// NT/64/WPR rows at a time; units (rows, or row pairs) are dealt to the block's
+// row slots round-robin over the grid.
+//
+// Each thread first issues the loads of its activation blocks, then the loads
+// of its first unit's packed bytes; the table is built while those are in
+// flight (a wave's loads return in order, so the table waits only for x).
+//
+// NORM:   x is the f32 residual stream; h = f16(x * rms * w) is formed in
+//         registers (the RMS with the same reduction as wst_rmsnorm), block 0
+//         also stores h when h_out is non-null. Requires NT == NORM_THREADS.
+// SWIGLU: nunits is the intermediate width; the unit writes f16(silu(g) * u).
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU>
+__global__ __launch_bounds__(NT) void gemv_hier_kernel(
     const uint4 *__restrict__ qw, const uint8_t *__restrict__ si,
     const uint32_t *__restrict__ sb, const void *__restrict__ xin,
     const uint16_t *__restrict__ norm_w, float eps, uint16_t *__restrict__ h_out,
-    const uint16_t *__restrict__ bias, void *__restrict__ yout, int in_f, int out_f, int accum,
-    uint32_t magic) {
-  constexpr int SLOTS = 64 / LPR;    // row-slots per wave
-  constexpr int NR = SWIGLU ? 2 : 1;  // matrix rows per unit row
+    const uint16_t *__restrict__ bias, void *__restrict__ yout, int in_f, int nunits,
+    int accum) {
+  static_assert(!NORM || NT == NORM_THREADS, "the RMS reduction order assumes 512 threads");
+  constexpr int NR = SWIGLU ? 2 : 1;
+  constexpr int NW = NT / 64;
+  constexpr int RPB = NW / WPR;
+  constexpr int LPR = 64 * WPR;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int slot = lane / LPR, lr = lane % LPR;
-  const int G = in_f / HGROUP;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rs = wave / WPR;
+  const int lr = (wave % WPR) * 64 + lane;
+  const int G = in_f / HGROUP, NB8 = in_f / 8;
+  __shared__ float red[2][NW][NR];
+  __shared__ float bred[16];
+  extern __shared__ uint32_t xgt[];  // [G][XQ_WORDS]
 
-  __shared__ float red[16];
-  extern __shared__ uint32_t xgt[];  // [G][XG_WORDS]
-
-  // ---- prologue: the x table
-  float s = 0.0f;
-  if constexpr (NORM) {
-    // rms_scale256's reduction, spread over 512 threads with the upper 256
-    // contributing exact zeros: same bits as the RMSNorm kernel.
-    // The first 16 strided values are loaded together (one round trip), then
-    // accumulated in index order.
-    const float *x = (const float *)xin;
-    float acc = 0.0f;
-    if (tid < 256) {
-      float v[16];
+  // 1. this thread's activation blocks b = tid + NT*i (and norm gains)
+  float xf[NORM ? XB : 1][8];
+  uint4 xh[NORM ? 1 : XB];
+  uint4 nwv[NORM ? XB : 1];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int i = tid + 256 * k;
-        v[k] = i < in_f ? x[i] : 0.0f;
-      }
-#pragma unroll
-      for (int k = 0; k < 16; ++k)
-        if (tid + 256 * k < in_f) acc = fmaf(v[k], v[k], acc);
-      for (int i = tid + 256 * 16; i < in_f; i += 256) acc = fmaf(x[i], x[i], acc);
-    }
-    s = 1.0f / sqrtf(block_sum(acc, red) / (float)in_f + eps);
-  }
-  for (int g = tid; g < G; g += GEMV_THREADS) {
-    uint32_t r[16];
-    if constexpr (NORM) {
-      const float4 *xv = (const float4 *)((const float *)xin + (size_t)g * HGROUP);
-      const uint4 *wv = (const uint4 *)(norm_w + (size_t)g * HGROUP);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 a = xv[2 * i], b = xv[2 * i + 1];
-        const uint4 ww = wv[i];
-        const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        const uint32_t wp[4] = {ww.x, ww.y, ww.z, ww.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint16_t lo = f2h(xs[2 * k] * s * h2f((uint16_t)(wp[k] & 0xFFFFu)));
-          const uint16_t hi = f2h(xs[2 * k + 1] * s * h2f((uint16_t)(wp[k] >> 16)));
-          r[4 * i + k] = (uint32_t)lo | ((uint32_t)hi << 16);
-        }
-      }
-      if (h_out && blockIdx.x == 0) {
-        uint4 *hv = (uint4 *)(h_out + (size_t)g * HGROUP);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          hv[i] = make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+  for (int i = 0; i < XB; ++i) {
+    const int b = tid + NT * i;
+    if (b < NB8) {
+      if constexpr (NORM) {
+        const float4 *xv = (const float4 *)((const float *)xin + (size_t)b * 8);
+        const float4 a = xv[0], c = xv[1];
+        xf[i][0] = a.x; xf[i][1] = a.y; xf[i][2] = a.z; xf[i][3] = a.w;
+        xf[i][4] = c.x; xf[i][5] = c.y; xf[i][6] = c.z; xf[i][7] = c.w;
+        nwv[i] = *(const uint4 *)(norm_w + (size_t)b * 8);
+      } else {
+        xh[i] = *(const uint4 *)((const uint16_t *)xin + (size_t)b * 8);
       }
     } else {
-      const uint4 *xv = (const uint4 *)((const uint16_t *)xin + (size_t)g * HGROUP);
+      if constexpr (NORM) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint4 v = xv[i];
-        r[4 * i] = v.x;
-        r[4 * i + 1] = v.y;
-        r[4 * i + 2] = v.z;
-        r[4 * i + 3] = v.w;
+        for (int e = 0; e < 8; ++e) xf[i][e] = 0.0f;
+        nwv[i] = make_uint4(0, 0, 0, 0);
+      } else {
+        xh[i] = make_uint4(0, 0, 0, 0);
       }
     }
-    XGroup xg;
-    build_xgroup(r, xg);
-    store_xgroup(xgt + (size_t)g * XG_WORDS, xg);
+  }
+
+  // 2. the first unit's packed bytes
+  const int stride = gridDim.x * RPB;
+  int base = blockIdx.x * RPB;
+  uint4 wq[NR][NG];
+  uint32_t idx[NR][NG];
+  uint32_t sbv[NR];
+  auto load_unit = [&](int row) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const int r = row + k * nunits;
+      sbv[k] = sb[r];
+      const uint4 *qr = qw + (size_t)r * G;
+      const uint8_t *sr = si + (size_t)r * G;
+#pragma unroll
+      for (int j = 0; j < NG; ++j) {
+        const int g = lr + j * LPR;
+        if (g < G) {
+          wq[k][j] = ld_stream16(qr + g);
+          idx[k][j] = sr[g];
+        } else {
+          wq[k][j] = make_uint4(0, 0, 0, 0);
+          idx[k][j] = 0;
+        }
+      }
+    }
+  };
+  if (base + rs < nunits) load_unit(base + rs);
+
+  // 3. the RMS scale (rms_scale512's order: thread t, blocks t, t+512, ...)
+  float s = 1.0f;
+  if constexpr (NORM) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XB; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf(xf[i][e], xf[i][e], acc);
+    s = 1.0f / sqrtf(block_sum(acc, bred) / (float)in_f + eps);
+  }
+
+  // 4. the table
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int b = tid + NT * i;
+    uint16_t h[8];
+    if constexpr (NORM) {
+      const uint32_t nw[4] = {nwv[i].x, nwv[i].y, nwv[i].z, nwv[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        h[2 * k] = f2h(xf[i][2 * k] * s * h2f((uint16_t)(nw[k] & 0xFFFFu)));
+        h[2 * k + 1] = f2h(xf[i][2 * k + 1] * s * h2f((uint16_t)(nw[k] >> 16)));
+      }
+      if (h_out && blockIdx.x == 0 && b < NB8)
+        *(uint4 *)(h_out + (size_t)b * 8) =
+            make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                       h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+    } else {
+      const uint32_t w[4] = {xh[i].x, xh[i].y, xh[i].z, xh[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        h[2 * k] = (uint16_t)(w[k] & 0xFFFFu);
+        h[2 * k + 1] = (uint16_t)(w[k] >> 16);
+      }
+    }
+    build_xq(h, b, b < NB8, xgt);
   }
   __syncthreads();
 
-  // ---- rows
-  const int nunits = (out_f + SLOTS * TILE - 1) / (SLOTS * TILE);
-  const int tw = gridDim.x * (GEMV_THREADS / 64);
-  for (int unit = blockIdx.x * (GEMV_THREADS / 64) + (tid >> 6); unit < nunits; unit += tw) {
-    const int row0 = (unit * SLOTS + slot) * TILE;
-    uint4 wq[TILE][NR][NG];
-    uint32_t idx[TILE][NR][NG];
-    uint32_t sbv[TILE][NR];
+  // 5. rows. The trip count is the same for every wave of the block (the
+  // WPR > 1 reduction synchronises the block).
+  for (int it = 0; base < nunits; base += stride, ++it) {
+    const int row = base + rs;
+    float as[NR], am[NR];
 #pragma unroll
-    for (int t = 0; t < TILE; ++t) {
-      const bool rv = row0 + t < out_f;
-#pragma unroll
-      for (int k = 0; k < NR; ++k) {
-        const int r = row0 + t + k * out_f;
-        sbv[t][k] = rv ? sb[r] : 0u;
-#pragma unroll
-        for (int j = 0; j < NG; ++j) {
-          const int g = lr + j * LPR;
-          const size_t at = (size_t)r * G + g;
-          if (rv && g < G) {
-            wq[t][k][j] = ld_stream16(qw + at);
-            idx[t][k][j] = si[at];
-          } else {
-            wq[t][k][j] = make_uint4(0, 0, 0, 0);
-            idx[t][k][j] = 0;
-          }
-        }
-      }
-    }
-    float as[TILE][NR], am[TILE][NR];
-#pragma unroll
-    for (int t = 0; t < TILE; ++t)
-#pragma unroll
-      for (int k = 0; k < NR; ++k) as[t][k] = am[t][k] = 0.0f;
+    for (int k = 0; k < NR; ++k) as[k] = am[k] = 0.0f;
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
       const int g = lr + j * LPR;
       if (g >= G) continue;
-      XGroup xg;
-      load_xgroup_lds(xgt + (size_t)g * XG_WORDS, xg);
-#pragma unroll
-      for (int t = 0; t < TILE; ++t)
-#pragma unroll
-        for (int k = 0; k < NR; ++k) {
-          const float q = group_dot(wq[t][k][j], xg, magic);
-          as[t][k] = fmaf((float)(idx[t][k][j] & 0xFu), q, as[t][k]);
-          am[t][k] = fmaf((float)(idx[t][k][j] >> 4), xg.sum, am[t][k]);
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < TILE; ++t) {
-      float part[NR];
+      const uint32_t *e = xgt + (size_t)g * XQ_WORDS;
+      const uint4 l0 = *(const uint4 *)(e), l1 = *(const uint4 *)(e + 4);
+      const uint4 l2 = *(const uint4 *)(e + 8), l3 = *(const uint4 *)(e + 12);
+      const int c8 = (int)e[16];
+      const float S = __uint_as_float(e[17]), sc = __uint_as_float(e[18]);
 #pragma unroll
       for (int k = 0; k < NR; ++k) {
-        const float d = h2f((uint16_t)(sbv[t][k] & 0xFFFFu));
-        const float dm = h2f((uint16_t)(sbv[t][k] >> 16));
-        part[k] = slot_sum<LPR>(d * as[t][k] - dm * am[t][k]);
+        const uint4 p = wq[k][j];
+        const uint32_t w0 = p.x ^ 0x88888888u, w1 = p.y ^ 0x88888888u;
+        const uint32_t w2 = p.z ^ 0x88888888u, w3 = p.w ^ 0x88888888u;
+        int a0 = sdot8(w0, l0.x, c8), a1 = sdot8z(w0, l0.y);
+        int a2 = sdot8z(w0, l0.z), a3 = sdot8z(w0, l0.w);
+        a0 = sdot8(w1, l1.x, a0); a1 = sdot8(w1, l1.y, a1);
+        a2 = sdot8(w1, l1.z, a2); a3 = sdot8(w1, l1.w, a3);
+        a0 = sdot8(w2, l2.x, a0); a1 = sdot8(w2, l2.y, a1);
+        a2 = sdot8(w2, l2.z, a2); a3 = sdot8(w2, l2.w, a3);
+        a0 = sdot8(w3, l3.x, a0); a1 = sdot8(w3, l3.y, a1);
+        a2 = sdot8(w3, l3.z, a2); a3 = sdot8(w3, l3.w, a3);
+        const int t = a0 + (a1 << 4) + (a2 << 8) + (a3 << 12);  // sum_i q_i X_i
+        const uint32_t id = idx[k][j];
+        as[k] = fmaf((float)(id & 0xFu) * sc, (float)t, as[k]);
+        am[k] = fmaf((float)(id >> 4), S, am[k]);
       }
-      const int r = row0 + t;
-      if (lr == 0 && r < out_f) {
-        if constexpr (SWIGLU) {
-          const float g = part[0], up = part[NR - 1];
-          ((uint16_t *)yout)[r] = f2h(g / (1.0f + __expf(-g)) * up);
-        } else {
-          float v = part[0];
-          if (bias) v += h2f(bias[r]);
-          float *y = (float *)yout;
-          y[r] = accum ? y[r] + v : v;
+    }
+    float lv[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const float d = h2f((uint16_t)(sbv[k] & 0xFFFFu));
+      const float dm = h2f((uint16_t)(sbv[k] >> 16));
+      lv[k] = d * as[k] - dm * am[k];
+    }
+    // The next unit's loads go out before this one's reductions and stores.
+    if (base + stride + rs < nunits) load_unit(base + stride + rs);
+    float part[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) part[k] = wave_sum(lv[k]);
+    if constexpr (WPR > 1) {
+      if (lane == 0)
+#pragma unroll
+        for (int k = 0; k < NR; ++k) red[it & 1][wave][k] = part[k];
+      __syncthreads();
+      if (lane == 0 && (wave % WPR) == 0) {
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+          float v = red[it & 1][wave][k];
+#pragma unroll
+          for (int w = 1; w < WPR; ++w) v += red[it & 1][wave + w][k];
+          part[k] = v;
         }
+      }
+    }
+    if (lane == 0 && (wave % WPR) == 0 && row < nunits) {
+      if constexpr (SWIGLU) {
+        const float g = part[0], up = part[NR - 1];
+        ((uint16_t *)yout)[row] = f2h(g / (1.0f + __expf(-g)) * up);
+      } else {
+        float v = part[0];
+        if (bias) v += h2f(bias[row]);
+        float *y = (float *)yout;
+        y[row] = accum ? y[row] + v : v;
       }
     }
   }
@@ -357,10 +478,10 @@ __global__ __launch_bounds__(256) void gemv_hier_wide_kernel(
 
 // ---------------------------------------------------------------- dispatch
 
-// Tile rule (wide reduction, huge output, everything else), entries 0..3 ->
-// TILE 1, 2, 4, 8 rows per row-slot, clamped so a lane holds at most 16
-// groups per unit. Same knob and classes as the reference
-// (gemv_hier.cu:253-272); the defaults are this kernel's own.
+// The (wide, huge, other) rule of the reference (gemv_hier.cu:253-272) picks
+// rows per thread tile there. This kernel's mapping depends only on in_f, so
+// the rule is kept (and reported) for API compatibility but selects nothing:
+// every rule gives the same bits, as the reference requires of its rules.
 static int g_hier_rule[3] = {0, 0, 1};
 
 extern "C" void wst_gemv_hier_set_rule(int32_t wide, int32_t huge, int32_t other) {
@@ -376,20 +497,14 @@ extern "C" void wst_gemv_hier_get_rule(int32_t *out) {
   out[2] = g_hier_rule[2];
 }
 
-static int hier_tile_index(int in_f, int rows) {
-  if (in_f >= 2048) return g_hier_rule[0];
-  if (rows >= 65536) return g_hier_rule[1];
-  return g_hier_rule[2];
-}
-
-// Blocks per CU of the persistent grid. WST_GEMV_BLOCKS_PER_CU overrides the
-// default (for sweeps).
+// Upper bound on resident blocks per CU used to size the persistent grid.
+// WST_GEMV_BLOCKS_PER_CU overrides it (for sweeps).
 static int blocks_per_cu() {
   static int v = 0;
   if (v == 0) {
     const char *e = getenv("WST_GEMV_BLOCKS_PER_CU");
     v = e ? atoi(e) : 0;
-    if (v <= 0 || v > 64) v = 4;
+    if (v <= 0 || v > 64) v = 2;
   }
   return v;
 }
@@ -401,51 +516,55 @@ struct HierArgs {
   void *h_out;
   const void *bias;
   void *y;
-  int in_f, out_f, accum;
+  int in_f, nunits, accum;
 };
 
-template <int LPR, int NG, int TILE, bool NORM, bool SWIGLU>
-static void launch_t(const HierArgs &a) {
-  const int rows_per_wave = (64 / LPR) * TILE;
-  const int units = (a.out_f + rows_per_wave - 1) / rows_per_wave;
-  const int blocks = (units + GEMV_THREADS / 64 - 1) / (GEMV_THREADS / 64);
-  const int cap = wst_cu_count() * blocks_per_cu();
-  const int grid = blocks < cap ? blocks : cap;
-  const size_t lds = (size_t)(a.in_f / HGROUP) * XG_WORDS * 4;
-  gemv_hier_kernel<LPR, NG, TILE, NORM, SWIGLU><<<grid, GEMV_THREADS, lds, WST_STREAM>>>(
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU>
+static void launch_q(const HierArgs &a) {
+  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU>;
+  const size_t lds = (size_t)(a.in_f / HGROUP) * XQ_WORDS * 4;
+  // Resident blocks per CU for this instance and LDS size, queried once.
+  static thread_local size_t q_lds = (size_t)-1;
+  static thread_local int q_res = 1;
+  if (lds != q_lds) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, NT, lds) != hipSuccess || n <= 0)
+      n = 1;
+    q_res = n < blocks_per_cu() ? n : blocks_per_cu();
+    q_lds = lds;
+  }
+  // Balanced persistent grid: at most k units per row slot, and just enough
+  // blocks that every slot gets k (or k-1), so no tail round runs a fraction
+  // of the slots.
+  constexpr int RPB = NT / 64 / WPR;
+  const int cap = wst_cu_count() * q_res * RPB;
+  const int k = (a.nunits + cap - 1) / cap;
+  const int grid = (a.nunits + k * RPB - 1) / (k * RPB);
+  kern<<<grid, NT, lds, WST_STREAM>>>(
       (const uint4 *)a.qw, (const uint8_t *)a.si, (const uint32_t *)a.sb, a.x,
       (const uint16_t *)a.norm_w, a.eps, (uint16_t *)a.h_out, (const uint16_t *)a.bias, a.y,
-      a.in_f, a.out_f, a.accum, HIER_MAGIC);
+      a.in_f, a.nunits, a.accum);
 }
 
-template <int LPR, int NG, bool NORM, bool SWIGLU>
-static void launch_tile(int tile_idx, const HierArgs &a) {
-  constexpr int NR = SWIGLU ? 2 : 1;
-  int t = tile_idx;
-  while (t > 0 && (1 << t) * NG * NR > 16) --t;  // register budget
-  switch (t) {
-    case 0: launch_t<LPR, NG, 1, NORM, SWIGLU>(a); break;
-    case 1: if constexpr (2 * NG * NR <= 16) launch_t<LPR, NG, 2, NORM, SWIGLU>(a); break;
-    case 2: if constexpr (4 * NG * NR <= 16) launch_t<LPR, NG, 4, NORM, SWIGLU>(a); break;
-    default: if constexpr (8 * NG * NR <= 16) launch_t<LPR, NG, 8, NORM, SWIGLU>(a); break;
-  }
-}
-
-// Shape -> (lanes per row, groups per lane).
+// in_f -> (groups per lane, waves per row, activation blocks per thread,
+// threads). NORM forms use 512 threads (their RMS order); plain forms with
+// long rows use 1024 so a CU builds its table once.
+#define GEMV_MAX_G 1280  // groups per row handled by the table kernel
 template <bool NORM, bool SWIGLU>
-static bool hier_dispatch(int tile_idx, const HierArgs &a) {
+static bool hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
-  const int ng = (G + 63) / 64;
-  if (G <= 32) launch_tile<32, 1, NORM, SWIGLU>(tile_idx, a);
-  else if (ng == 1) launch_tile<64, 1, NORM, SWIGLU>(tile_idx, a);
-  else if (ng == 2) launch_tile<64, 2, NORM, SWIGLU>(tile_idx, a);
-  else if (ng == 3) launch_tile<64, 3, NORM, SWIGLU>(tile_idx, a);
-  else if (ng == 4) launch_tile<64, 4, NORM, SWIGLU>(tile_idx, a);
-  else if (ng <= 6) launch_tile<64, 6, NORM, SWIGLU>(tile_idx, a);
-  else if (ng <= 8) launch_tile<64, 8, NORM, SWIGLU>(tile_idx, a);
-  else if (ng <= 10) launch_tile<64, 10, NORM, SWIGLU>(tile_idx, a);
-  else if (ng <= 12) launch_tile<64, 12, NORM, SWIGLU>(tile_idx, a);
-  else return false;
+  if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU>(a);
+  else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU>(a);
+  else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU>(a);
+  else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU>(a);
+  else if constexpr (NORM) {
+    if (G <= 512) launch_q<4, 2, 4, 512, NORM, SWIGLU>(a);
+    else return false;
+  } else {
+    if (G <= 640) launch_q<5, 2, 3, 1024, NORM, SWIGLU>(a);
+    else if (G <= GEMV_MAX_G) launch_q<5, 4, 5, 1024, NORM, SWIGLU>(a);
+    else return false;
+  }
   return true;
 }
 
@@ -477,7 +596,7 @@ extern "C" wst_status_t wst_gemv_int4_hier_ex(const void *qw, const void *si, co
   const wst_status_t st = check_common(qw, si, sb, x, y, in_f, out_f, "wst_gemv_int4_hier");
   if (st != WST_OK) return st;
   const HierArgs a{qw, si, sb, x, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum};
-  if (in_f / HGROUP > GEMV_MAX_G || !hier_dispatch<false, false>(hier_tile_index(in_f, out_f), a)) {
+  if (!hier_dispatch<false, false>(a)) {
     const int units = (out_f + 3) / 4;
     const int cap = wst_cu_count() * 16;
     gemv_hier_wide_kernel<4><<<units < cap ? units : cap, 256, 0, WST_STREAM>>>(
@@ -495,11 +614,11 @@ extern "C" wst_status_t wst_gemv_hier_rmsnorm(const void *qw, const void *si, co
   const wst_status_t st = check_common(qw, si, sb, x, y, in_f, out_f, "wst_gemv_hier_rmsnorm");
   if (st != WST_OK) return st;
   WST_REQUIRE(norm_w, "wst_gemv_hier_rmsnorm: null norm weight");
-  WST_REQUIRE(in_f / HGROUP <= GEMV_MAX_G, "wst_gemv_hier_rmsnorm: in_features above 24576");
+  WST_REQUIRE(in_f / HGROUP <= 512, "wst_gemv_hier_rmsnorm: in_features above 16384");
   WST_REQUIRE(!(((uintptr_t)norm_w | (uintptr_t)h_out) & 15u),
               "wst_gemv_hier_rmsnorm: norm weight and h must be 16-byte aligned");
   const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, bias, y, in_f, out_f, accum};
-  hier_dispatch<true, false>(hier_tile_index(in_f, out_f), a);
+  hier_dispatch<true, false>(a);
   WST_TRY_KERNEL("wst_gemv_hier_rmsnorm");
   return WST_OK;
 }
@@ -509,12 +628,12 @@ extern "C" wst_status_t wst_gemv_hier_swiglu(const void *qw, const void *si, con
                                              void *out, int32_t in_f, int32_t inter) {
   const wst_status_t st = check_common(qw, si, sb, x, out, in_f, inter, "wst_gemv_hier_swiglu");
   if (st != WST_OK) return st;
-  WST_REQUIRE(in_f / HGROUP <= GEMV_MAX_G, "wst_gemv_hier_swiglu: in_features above 24576");
+  WST_REQUIRE(in_f / HGROUP <= (norm_w ? 512 : GEMV_MAX_G),
+              "wst_gemv_hier_swiglu: in_features above 16384 (40960 without the norm)");
   WST_REQUIRE(!((uintptr_t)norm_w & 15u), "wst_gemv_hier_swiglu: norm weight must be 16-byte aligned");
   const HierArgs a{qw, si, sb, x, norm_w, eps, nullptr, nullptr, out, in_f, inter, 0};
-  const int ti = hier_tile_index(in_f, 2 * inter);
-  if (norm_w) hier_dispatch<true, true>(ti, a);
-  else hier_dispatch<false, true>(ti, a);
+  if (norm_w) hier_dispatch<true, true>(a);
+  else hier_dispatch<false, true>(a);
   WST_TRY_KERNEL("wst_gemv_hier_swiglu");
   return WST_OK;
 }
