@@ -73,7 +73,8 @@ wst_status_t wst_gemv_hier_swiglu(const void *qw, const void *si, const void *sb
                                   const void *x, const void *norm_w, float eps,
                                   void *out, int32_t in_f, int32_t inter);
 
-/* wst_rope_cache + wst_attn_decode in one launch. */
+/* wst_rope_cache + wst_attn_decode: the slice kernel (RoPE, KV append,
+ * per-slice softmax on MFMA) then the slice merge. */
 wst_status_t wst_attn_decode_fused(void *qkv, void *k_cache, void *v_cache,
                                    const void *cos_tab, const void *sin_tab, void *partials,
                                    void *out, int32_t n_q, int32_t n_kv, int32_t head_dim,

@@ -7,23 +7,23 @@
 // * One 512-thread block per (kv head, slice of P cached positions), P*hd =
 //   16384 (P = 256 / 128 / 64 at hd 64 / 128 / 256). Every K/V row is read
 //   from memory once and used for all n_q/n_kv query heads of the group.
-// * The block stages its slice of K and V in LDS (32 KB each) with one batch of
-//   16-byte loads -- one memory round trip -- and then works from LDS:
-//     scores   a lane per position, the wave's 64 positions against one query
-//              head at a time (q broadcast from LDS): hd FMAs per score, no
-//              cross-lane reduction;
-//     softmax  a wave per query head over the slice: one max, one exp per
-//              (head, position), one sum;
-//     P.V      a lane per (head, 8 output dims, 32 positions), reduced over the
-//              position groups through LDS.
-//   So each exp is computed once (the previous lane-per-dimension layout
-//   recomputed the online-softmax exps on every lane of a position and was
-//   compute bound).
-// * Slices merge in the last block of each kv head to finish (a device-scope
-//   counter that the merging block resets: the whole attention is one launch
-//   and needs no memset inside a graph), fetching the partials in batches of
-//   16 slices per round trip and combining them in slice order. A context
-//   that fits one slice skips the partials entirely.
+// * The block stages its slice in LDS with one batch of 16-byte loads (K as
+//   rows of positions, V transposed: rows of dims) and computes both products
+//   on MFMA (v_mfma_f32_16x16x32_f16, f32 accumulate):
+//     scores  S[h][p] = q_h . k_p : rows the block's heads (padded to 16),
+//             16 positions per tile;
+//     softmax a wave per head: one max, one exp per (head, position), one sum;
+//     P.V     O[h][d] = sum_p P[h][p] V[p][d] : 16 dims per tile.
+//   q and P enter the MFMA as their f16 hi part plus the f16 rounding of the
+//   rest, so the products keep ~22 bits; K and V are f16 already. The f32
+//   FMA formulation of the same block spent ~4 us of a 7.8 us single-slice
+//   launch on VALU; on MFMA the compute is a few hundred cycles.
+// * Each slice writes its unnormalised numerators and (max, sum) to the
+//   partials; a second kernel (one 64-thread block per head and 32 dims)
+//   merges the slices in slice order. Measured against merging in the last
+//   block of each kv head to finish: that costs a device-scope hand-off plus
+//   one CU pulling all of a kv head's partials, about 4.7 us; the separate
+//   merge about 3.
 // * The grid covers max_seq; only the ceil(seq/P) slices holding cached
 //   positions do work, so a captured graph serves every position.
 // * ROPE form (wst_attn_decode_fused): each block applies QK-norm and RoPE to
@@ -36,6 +36,8 @@
 // * Deterministic: every sum runs in a fixed order.
 #include "common.hpp"
 
+#include <stdlib.h>
+
 #define ATTN_THREADS 512
 #define ATTN_WAVES 8
 #define ATTN_MAX_GQA 8
@@ -44,25 +46,40 @@
 
 template <int HD>
 struct AttnShape {
-  static constexpr int P = ATTN_TILE / HD;                  // positions per block
-  static constexpr int KS = HD + 8;                         // K row stride (halves): +16 B
-  static constexpr int G = ATTN_THREADS / P;                // head groups, score phase
-  static constexpr int WPG = P / 64;                        // waves per head group
-  static constexpr int HPT = (ATTN_MAX_GQA + G - 1) / G;    // heads per lane, score phase
-  static constexpr int PG = ATTN_THREADS / HD;              // position groups, P.V phase
-  static constexpr int PPG = P / PG;                        // positions per group (32)
-  static constexpr int CH = HD / 8;                         // 16-byte chunks per row
-  // LDS (bytes): K tile | V tile | q (scaled) | scores | per-head (m, l)
+  static constexpr int P = ATTN_TILE / HD;  // positions per block
+  static constexpr int CH = HD / 8;         // 16-byte chunks per row
+  // Row strides in halves, padded by 16 bytes so that the 16 rows an MFMA
+  // operand read touches fall in different LDS banks.
+  static constexpr int KS = HD + 8;  // K tile  [P][KS]      (rows: positions)
+  static constexpr int VS = P + 8;   // V^T tile [HD][VS]    (rows: dims)
+  static constexpr int QS = HD + 8;  // q hi/lo  [16][QS]    (rows: heads)
+  static constexpr int PS = P + 8;   // p hi/lo  [16][PS]    (rows: heads)
   static constexpr int K_OFF = 0;
   static constexpr int V_OFF = K_OFF + P * KS * 2;
-  static constexpr int Q_OFF = V_OFF + P * HD * 2;
-  static constexpr int S_OFF = Q_OFF + ATTN_MAX_GQA * HD * 4;
-  static constexpr int ML_OFF = S_OFF + ATTN_MAX_GQA * P * 4;
-  static constexpr int LDS = ML_OFF + ATTN_MAX_GQA * 2 * 4;
-  // The P.V reduction buffer [PG][8][HD] f32 reuses the K tile.
-  static_assert(PG * ATTN_MAX_GQA * HD * 4 <= P * KS * 2, "reduction buffer fits the K tile");
-  static_assert(PPG == 32, "32 positions per P.V group");
+  static constexpr int QH_OFF = V_OFF + HD * VS * 2;
+  static constexpr int QL_OFF = QH_OFF + 16 * QS * 2;
+  static constexpr int S_OFF = QL_OFF + 16 * QS * 2;   // scores [16][P] f32
+  static constexpr int PH_OFF = S_OFF + 16 * P * 4;
+  static constexpr int PL_OFF = PH_OFF + 16 * PS * 2;
+  static constexpr int ML_OFF = PL_OFF + 16 * PS * 2;  // per head (m, l)
+  static constexpr int LDS = ML_OFF + 16 * 2 * 4;
+  static_assert(P % 32 == 0 && HD % 32 == 0, "MFMA tiles");
 };
+
+// Query-head groups per kv head (grid z): the heads of a kv head are split over
+// this many blocks per slice, each staging the same K/V tile, so that a slice's
+// score and P.V work is spread over more CUs. WST_ATTN_HEAD_GROUPS overrides.
+static int attn_head_groups(int gqa) {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("WST_ATTN_HEAD_GROUPS");
+    v = e ? atoi(e) : 0;
+  }
+  int z = v > 0 ? v : 1;
+  z = z < gqa ? z : gqa;
+  const int hpz = (gqa + z - 1) / z;  // heads per group; every group gets >= 1
+  return (gqa + hpz - 1) / hpz;
+}
 
 static inline int attn_slices(int head_dim, int max_seq) {
   const int p = ATTN_TILE / head_dim;
@@ -84,24 +101,46 @@ __device__ __forceinline__ void unpack8(const uint4 v, float *f) {
   }
 }
 
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Eight halves (16 bytes) from LDS as an MFMA operand.
+__device__ __forceinline__ h16x8 lds_h8(const uint16_t *p) {
+  return __builtin_bit_cast(h16x8, *(const uint4 *)p);
+}
+
+// q (already scaled) as its f16 hi part and the f16 rounding of the rest.
+__device__ __forceinline__ void store_q(uint16_t *qh, uint16_t *ql, int at, float v) {
+  const uint16_t h = f2h(v);
+  qh[at] = h;
+  ql[at] = f2h(v - h2f(h));
+}
+
 template <int HD, bool ROPE>
 __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
     const float *__restrict__ qkv, uint16_t *__restrict__ k_cache,
-    uint16_t *__restrict__ v_cache, float *__restrict__ partials, uint16_t *__restrict__ out,
-    unsigned int *__restrict__ counters, int n_q, int n_kv,
+    uint16_t *__restrict__ v_cache, float *__restrict__ partials, int n_q, int n_kv,
     const int32_t *__restrict__ pos_dev, int max_seq, float scale, RopeArgs ra) {
   using S = AttnShape<HD>;
   constexpr int P = S::P, CH = S::CH;
+  (void)CH;
   extern __shared__ __align__(16) unsigned char lds[];
   uint16_t *ktile = (uint16_t *)(lds + S::K_OFF);
   uint16_t *vtile = (uint16_t *)(lds + S::V_OFF);
-  float *qs = (float *)(lds + S::Q_OFF);
+  uint16_t *qh = (uint16_t *)(lds + S::QH_OFF);
+  uint16_t *ql = (uint16_t *)(lds + S::QL_OFF);
   float *sc = (float *)(lds + S::S_OFF);
+  uint16_t *ph = (uint16_t *)(lds + S::PH_OFF);
+  uint16_t *pl = (uint16_t *)(lds + S::PL_OFF);
   float *ml = (float *)(lds + S::ML_OFF);
-  float *red = (float *)(lds + S::K_OFF);
 
   const int gqa = n_q / n_kv;
   const int kvh = blockIdx.x, split = blockIdx.y, nsplit = gridDim.y;
+  // This block's query heads: group blockIdx.z of the kv head's gqa heads.
+  const int hpz = (gqa + gridDim.z - 1) / gridDim.z;
+  const int h0 = blockIdx.z * hpz;
+  const int hb = min(hpz, gqa - h0);  // >= 1: the launch keeps gridDim.z <= gqa
+  const int qh0 = kvh * gqa + h0;     // first global query head
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
   const int pos = min(max(*pos_dev, 0), max_seq - 1);
@@ -135,10 +174,10 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
     const bool active = j < HALF;
     const float c = active ? ra.cos_tab[(size_t)pos * HALF + j] : 0.0f;
     const float s = active ? ra.sin_tab[(size_t)pos * HALF + j] : 0.0f;
-    for (int h = wave; h < gqa + 1; h += ATTN_WAVES) {
-      const bool is_k = h == gqa;
+    for (int h = wave; h < hb + 1; h += ATTN_WAVES) {
+      const bool is_k = h == hb;
       if (is_k && !owner) continue;
-      const float *src = is_k ? qkv + (size_t)(n_q + kvh) * HD : qkv + (size_t)(kvh * gqa + h) * HD;
+      const float *src = is_k ? qkv + (size_t)(n_q + kvh) * HD : qkv + (size_t)(qh0 + h) * HD;
       float x1 = active ? src[j] : 0.0f;
       float x2 = active ? src[j + HALF] : 0.0f;
       const uint16_t *g = is_k ? ra.k_norm_w : ra.q_norm_w;
@@ -155,32 +194,36 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
       if (!active) continue;
       const float lo = rope_lo(x1, x2, c, s), hi = rope_hi(x1, x2, c, s);
       if (!is_k) {
-        qs[h * HD + j] = lo * scale;
-        qs[h * HD + j + HALF] = hi * scale;
+        store_q(qh, ql, h * S::QS + j, lo * scale);
+        store_q(qh, ql, h * S::QS + j + HALF, hi * scale);
       } else {
         const float *vh = qkv + (size_t)(n_q + n_kv + kvh) * HD;
         knew = f2h(lo);
         knew2 = f2h(hi);
         vnew = f2h(vh[j]);
         vnew2 = f2h(vh[j + HALF]);
-        const size_t slot = ((size_t)kvh * max_seq + pos) * HD;
-        k_cache[slot + j] = knew;
-        k_cache[slot + j + HALF] = knew2;
-        v_cache[slot + j] = vnew;
-        v_cache[slot + j + HALF] = vnew2;
+        if (blockIdx.z == 0) {  // every head group forms the row; one appends it
+          const size_t slot = ((size_t)kvh * max_seq + pos) * HD;
+          k_cache[slot + j] = knew;
+          k_cache[slot + j + HALF] = knew2;
+          v_cache[slot + j] = vnew;
+          v_cache[slot + j + HALF] = vnew2;
+        }
       }
     }
   } else {
     // At most 8 * 256 values: four unconditional (clamped) loads per thread,
     // so they share one round trip.
     constexpr int QL = ATTN_MAX_GQA * HD / ATTN_THREADS;
-    const int nqv = gqa * HD;
+    const int nqv = hb * HD;
     float qv[QL];
 #pragma unroll
-    for (int i = 0; i < QL; ++i) qv[i] = qkv[(size_t)kvh * nqv + min(tid + i * ATTN_THREADS, nqv - 1)];
+    for (int i = 0; i < QL; ++i) qv[i] = qkv[(size_t)qh0 * HD + min(tid + i * ATTN_THREADS, nqv - 1)];
 #pragma unroll
-    for (int i = 0; i < QL; ++i)
-      if (tid + i * ATTN_THREADS < nqv) qs[tid + i * ATTN_THREADS] = qv[i] * scale;
+    for (int i = 0; i < QL; ++i) {
+      const int e = tid + i * ATTN_THREADS;
+      if (e < nqv) store_q(qh, ql, (e / HD) * S::QS + e % HD, qv[i] * scale);
+    }
   }
 
   // Tiles into LDS; rows past the cached positions are zero (their scores are
@@ -191,62 +234,50 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
     const uint32_t mk = t0 + row < t1 ? 0xFFFFFFFFu : 0u;  // a mask, not a select of
     const uint4 a = kr[i], b = vr[i];                      // addresses (which spills)
     *(uint4 *)(ktile + row * S::KS + ch * 8) = make_uint4(a.x & mk, a.y & mk, a.z & mk, a.w & mk);
-    *(uint4 *)(vtile + row * HD + ch * 8) = make_uint4(b.x & mk, b.y & mk, b.z & mk, b.w & mk);
+    const uint32_t vw[4] = {b.x & mk, b.y & mk, b.z & mk, b.w & mk};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {  // V^T: dims are rows
+      vtile[(ch * 8 + 2 * e) * S::VS + row] = (uint16_t)(vw[e] & 0xFFFFu);
+      vtile[(ch * 8 + 2 * e + 1) * S::VS + row] = (uint16_t)(vw[e] >> 16);
+    }
   }
   if constexpr (ROPE) {
     __syncthreads();  // the tile row of `pos` holds the cache's old contents
-    if (owner && wave == gqa % ATTN_WAVES && lane < HD / 2) {
+    if (owner && wave == hb % ATTN_WAVES && lane < HD / 2) {
       const int row = pos - t0;
       ktile[row * S::KS + lane] = knew;
       ktile[row * S::KS + lane + HD / 2] = knew2;
-      vtile[row * HD + lane] = vnew;
-      vtile[row * HD + lane + HD / 2] = vnew2;
+      vtile[lane * S::VS + row] = vnew;
+      vtile[(lane + HD / 2) * S::VS + row] = vnew2;
     }
   }
   __syncthreads();
 
-  // ---- phase B: scores. Wave w: head group g, positions pb..pb+63 (one per lane).
+  // ---- phase B: scores S[h][p] = q_h . k_p on MFMA (16x16x32 f16, f32
+  // accumulate): rows are the block's heads (up to 16; rows past hb carry
+  // whatever the LDS held and are never read back), columns 16 positions per
+  // tile, q as its f16 hi and lo parts so the products keep ~22 bits of q.
   {
-    const int g = wave / S::WPG;
-    const int p = (wave % S::WPG) * 64 + lane;
-    float s[S::HPT];
+    const int r16 = lane & 15, kq = (lane >> 4) * 8;
+    for (int nt = wave; nt < P / 16; nt += ATTN_WAVES) {
+      f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < S::HPT; ++i) s[i] = 0.0f;
-    const uint16_t *krow = ktile + p * S::KS;
-#pragma unroll 4
-    for (int c = 0; c < CH; ++c) {
-      float kf[8];
-      unpack8(*(const uint4 *)(krow + c * 8), kf);
-#pragma unroll
-      for (int i = 0; i < S::HPT; ++i) {
-        const int h = g + i * S::G;
-        if (h < gqa) {  // uniform across the wave
-          const float4 qa = *(const float4 *)(qs + h * HD + c * 8);
-          const float4 qb = *(const float4 *)(qs + h * HD + c * 8 + 4);
-          float a = s[i];
-          a = fmaf(qa.x, kf[0], a);
-          a = fmaf(qa.y, kf[1], a);
-          a = fmaf(qa.z, kf[2], a);
-          a = fmaf(qa.w, kf[3], a);
-          a = fmaf(qb.x, kf[4], a);
-          a = fmaf(qb.y, kf[5], a);
-          a = fmaf(qb.z, kf[6], a);
-          a = fmaf(qb.w, kf[7], a);
-          s[i] = a;
-        }
+      for (int kk = 0; kk < HD; kk += 32) {
+        const h16x8 b = lds_h8(ktile + (nt * 16 + r16) * S::KS + kk + kq);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(qh + r16 * S::QS + kk + kq), b, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(ql + r16 * S::QS + kk + kq), b, c, 0, 0, 0);
       }
-    }
-    const bool valid = t0 + p < t1;
+      const int p = nt * 16 + r16;
+      const bool valid = t0 + p < t1;
 #pragma unroll
-    for (int i = 0; i < S::HPT; ++i) {
-      const int h = g + i * S::G;
-      if (h < gqa) sc[h * P + p] = valid ? s[i] : -INFINITY;
+      for (int i = 0; i < 4; ++i) sc[((lane >> 4) * 4 + i) * P + p] = valid ? c[i] : -INFINITY;
     }
   }
   __syncthreads();
 
-  // ---- phase C: softmax over the slice, a wave per head.
-  if (wave < gqa) {
+  // ---- phase C: softmax over the slice, a wave per head; the weights go to
+  // LDS as f16 hi and lo parts for the P.V MFMAs.
+  if (wave < hb) {
     constexpr int R = P / 64;
     float v[R];
     float m = -INFINITY;
@@ -260,7 +291,9 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float e = (v[r] == -INFINITY) ? 0.0f : __expf(v[r] - m);
-      sc[wave * P + lane + 64 * r] = e;
+      const uint16_t eh = f2h(e);
+      ph[wave * S::PS + lane + 64 * r] = eh;
+      pl[wave * S::PS + lane + 64 * r] = f2h(e - h2f(eh));
       l += e;
     }
     l = wave_sum(l);
@@ -271,109 +304,110 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
   }
   __syncthreads();
 
-  // ---- phase D: P.V. Lane (position group pg, head h, 8 dims dc).
-  {
-    const int pg = tid / HD, rem = tid % HD, h = rem / CH, dc = rem % CH;
-    float acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    if (h < gqa) {
-      const float *w = sc + h * P + pg * S::PPG;
-      const uint16_t *vcol = vtile + (pg * S::PPG) * HD + dc * 8;
-#pragma unroll 8
-      for (int j = 0; j < S::PPG; ++j) {
-        const float pj = w[j];
-        float vf[8];
-        unpack8(*(const uint4 *)(vcol + j * HD), vf);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(pj, vf[i], acc[i]);
-      }
-    }
-    // K tile is dead since phase B: reuse it for the group reduction.
-    float4 *dst = (float4 *)(red + ((pg * ATTN_MAX_GQA + h) * HD + dc * 8));
-    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-  }
-  __syncthreads();
-
-  // ---- phase E: this slice's result.
+  // ---- phase D: O[h][d] = sum_p P[h][p] V[p][d] on MFMA (V^T rows are dims),
+  // then this slice's result straight from the accumulators.
   float *pacc = partials;
   float *pml = partials + (size_t)n_q * nsplit * HD;
-  for (int k = tid; k < gqa * HD; k += ATTN_THREADS) {
-    const int h = k / HD, d = k % HD;
-    float a = 0.0f;
+  {
+    const int r16 = lane & 15, kq = (lane >> 4) * 8;
+    for (int nd = wave; nd < HD / 16; nd += ATTN_WAVES) {
+      f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+      for (int kk = 0; kk < P; kk += 32) {
+        const h16x8 b = lds_h8(vtile + (nd * 16 + r16) * S::VS + kk + kq);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(ph + r16 * S::PS + kk + kq), b, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pl + r16 * S::PS + kk + kq), b, c, 0, 0, 0);
+      }
+      const int d = nd * 16 + r16;
 #pragma unroll
-    for (int pg = 0; pg < S::PG; ++pg) a += red[(pg * ATTN_MAX_GQA + h) * HD + d];
-    if (nactive == 1) {
-      out[(size_t)(kvh * gqa + h) * HD + d] = f2h(a / ml[h * 2 + 1]);
-    } else {
-      const size_t row = (size_t)(kvh * gqa + h) * nsplit + split;
-      pacc[row * HD + d] = a;
-      if (d == 0) {
-        pml[row * 2] = ml[h * 2];
-        pml[row * 2 + 1] = ml[h * 2 + 1];
+      for (int i = 0; i < 4; ++i) {
+        const int h = (lane >> 4) * 4 + i;
+        if (h >= hb) continue;
+        const size_t row = (size_t)(qh0 + h) * nsplit + split;
+        pacc[row * HD + d] = c[i];
+        if (d == 0) {
+          pml[row * 2] = ml[h * 2];
+          pml[row * 2 + 1] = ml[h * 2 + 1];
+        }
       }
     }
   }
-  if (nactive == 1) return;
-  if (!last_block_done(counters + kvh, (unsigned int)nactive)) return;
+}
 
-  // ---- slice merge for the gqa heads of this kv head (attention.cu:170-193):
-  // one thread per (head, 4 dims) fetches the slices' (m, l) and numerators in
-  // batches of ATTN_MERGE_BATCH (one round trip each) and combines them in
-  // slice order, rescaling the running sum when a batch raises the maximum.
-  for (int k = tid; k < gqa * (HD / 4); k += ATTN_THREADS) {
-    const int h = k / (HD / 4), d4 = k % (HD / 4);
-    const size_t row0 = (size_t)(kvh * gqa + h) * nsplit;
-    float M = -INFINITY, den = 0.0f;
-    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int c0 = 0; c0 < nactive; c0 += ATTN_MERGE_BATCH) {
-      float ms[ATTN_MERGE_BATCH], ls[ATTN_MERGE_BATCH];
-      float4 vs[ATTN_MERGE_BATCH];
-      // Unconditional loads (a clamped slice index) so that all of them are
-      // in flight together; guarded loads compile to one round trip each.
+// ---------------------------------------------------------------- slice merge
+//
+// out[h][d] = sum_s e^(m_s - M) acc_s[d] / sum_s e^(m_s - M) l_s with M the
+// largest slice maximum (attention.cu:170-193). One 64-thread block per (head,
+// 32 dims): lane (half, d) combines a contiguous half of the slices in slice
+// order, fetching ATTN_MERGE_BATCH of them per round trip; the two halves are
+// then combined in order.
+__global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ partials,
+                                                        uint16_t *__restrict__ out, int n_q, int hd,
+                                                        int nsplit,
+                                                        const int32_t *__restrict__ pos_dev,
+                                                        int max_seq, int P) {
+  __shared__ float hx[32][3];
+  const int h = blockIdx.x, d0 = blockIdx.y * 32, lane = threadIdx.x;
+  const int half = lane >> 5, d = d0 + (lane & 31);
+  const int seq = min(max(*pos_dev, 0) + 1, max_seq);
+  const int nactive = (seq + P - 1) / P;
+  const float *pacc = partials;
+  const float *pml = partials + (size_t)n_q * nsplit * hd;
+  const int run = (nactive + 1) / 2;
+  const int s0 = half * run, s1 = min(s0 + run, nactive);
+  const size_t row0 = (size_t)h * nsplit;
+  float M = -INFINITY, den = 0.0f, a = 0.0f;
+  for (int c0 = s0; c0 < s1; c0 += ATTN_MERGE_BATCH) {
+    float ms[ATTN_MERGE_BATCH], ls[ATTN_MERGE_BATCH], vs[ATTN_MERGE_BATCH];
+    // Unconditional loads (a clamped slice index) so that all of them are in
+    // flight together.
 #pragma unroll
-      for (int i = 0; i < ATTN_MERGE_BATCH; ++i) {
-        const int s = c0 + i;
-        const size_t r = row0 + (s < nactive ? s : nactive - 1);
-        const float2 mlv = *(const float2 *)(pml + r * 2);
-        ms[i] = s < nactive ? mlv.x : -INFINITY;
-        ls[i] = mlv.y;
-        vs[i] = ((const float4 *)(pacc + r * HD))[d4];
-      }
-      float Mn = M;
-#pragma unroll
-      for (int i = 0; i < ATTN_MERGE_BATCH; ++i) Mn = fmaxf(Mn, ms[i]);
-      const float fo = (M == -INFINITY) ? 0.0f : __expf(M - Mn);
-      a.x *= fo;
-      a.y *= fo;
-      a.z *= fo;
-      a.w *= fo;
-      den *= fo;
-#pragma unroll
-      for (int i = 0; i < ATTN_MERGE_BATCH; ++i) {
-        // slices past nactive carry m = -inf: f = 0 adds exact zeros
-        const float f = (ms[i] == -INFINITY) ? 0.0f : __expf(ms[i] - Mn);
-        a.x = fmaf(vs[i].x, f, a.x);
-        a.y = fmaf(vs[i].y, f, a.y);
-        a.z = fmaf(vs[i].z, f, a.z);
-        a.w = fmaf(vs[i].w, f, a.w);
-        den = fmaf(ls[i], f, den);
-      }
-      M = Mn;
+    for (int i = 0; i < ATTN_MERGE_BATCH; ++i) {
+      const int sl = c0 + i;
+      const size_t r = row0 + (sl < s1 ? sl : s1 - 1);
+      const float2 mlv = *(const float2 *)(pml + r * 2);
+      ms[i] = sl < s1 ? mlv.x : -INFINITY;
+      ls[i] = mlv.y;
+      vs[i] = pacc[r * hd + d];
     }
-    uint16_t *o = out + (size_t)(kvh * gqa + h) * HD + d4 * 4;
-    o[0] = f2h(a.x / den);
-    o[1] = f2h(a.y / den);
-    o[2] = f2h(a.z / den);
-    o[3] = f2h(a.w / den);
+    float Mn = M;
+#pragma unroll
+    for (int i = 0; i < ATTN_MERGE_BATCH; ++i) Mn = fmaxf(Mn, ms[i]);
+    const float fo = (M == -INFINITY) ? 0.0f : __expf(M - Mn);
+    a *= fo;
+    den *= fo;
+#pragma unroll
+    for (int i = 0; i < ATTN_MERGE_BATCH; ++i) {
+      // slices past the run carry m = -inf: f = 0 adds exact zeros
+      const float f = (ms[i] == -INFINITY) ? 0.0f : __expf(ms[i] - Mn);
+      a = fmaf(vs[i], f, a);
+      den = fmaf(ls[i], f, den);
+    }
+    M = Mn;
+  }
+  if (half == 1) {
+    hx[lane & 31][0] = M;
+    hx[lane & 31][1] = den;
+    hx[lane & 31][2] = a;
+  }
+  __syncthreads();
+  if (half == 0) {
+    const float Mt = hx[lane][0];
+    if (Mt != -INFINITY) {  // an empty second half adds nothing
+      const float Mn = fmaxf(M, Mt);
+      const float fo = (M == -INFINITY) ? 0.0f : __expf(M - Mn);
+      const float ft = __expf(Mt - Mn);
+      den = den * fo + hx[lane][1] * ft;
+      a = a * fo + hx[lane][2] * ft;
+    }
+    out[(size_t)h * hd + d] = f2h(a / den);
   }
 }
 
 template <int HD, bool ROPE>
 static void attn_go(const dim3 grid, const void *qkv, void *k_cache, void *v_cache,
-                    void *partials, void *out, unsigned int *counters, int n_q, int n_kv,
-                    const void *pos, int max_seq, float scale, const RopeArgs &ra) {
+                    void *partials, int n_q, int n_kv, const void *pos, int max_seq, float scale,
+                    const RopeArgs &ra) {
   static bool attr_set = false;
   if (!attr_set) {
     hipFuncSetAttribute((const void *)attn_decode_kernel<HD, ROPE>,
@@ -381,30 +415,34 @@ static void attn_go(const dim3 grid, const void *qkv, void *k_cache, void *v_cac
     attr_set = true;
   }
   attn_decode_kernel<HD, ROPE><<<grid, ATTN_THREADS, AttnShape<HD>::LDS, WST_STREAM>>>(
-      (const float *)qkv, (uint16_t *)k_cache, (uint16_t *)v_cache, (float *)partials,
-      (uint16_t *)out, counters, n_q, n_kv, (const int32_t *)pos, max_seq, scale, ra);
+      (const float *)qkv, (uint16_t *)k_cache, (uint16_t *)v_cache, (float *)partials, n_q,
+      n_kv, (const int32_t *)pos, max_seq, scale, ra);
 }
 
+// The slice kernel, then the merge.
 template <bool ROPE>
 static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_cache,
-                        void *partials, void *out, unsigned int *counters, int n_q, int n_kv,
-                        const void *pos, int max_seq, float scale, const RopeArgs &ra) {
-  const dim3 grid(n_kv, attn_slices(head_dim, max_seq));
+                        void *partials, void *out, int n_q, int n_kv, const void *pos,
+                        int max_seq, float scale, const RopeArgs &ra) {
+  const int nsplit = attn_slices(head_dim, max_seq);
+  const dim3 grid(n_kv, nsplit, attn_head_groups(n_q / n_kv));
   switch (head_dim) {
     case 64:
-      attn_go<64, ROPE>(grid, qkv, k_cache, v_cache, partials, out, counters, n_q, n_kv, pos,
-                        max_seq, scale, ra);
+      attn_go<64, ROPE>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv, pos, max_seq, scale, ra);
       break;
     case 128:
-      attn_go<128, ROPE>(grid, qkv, k_cache, v_cache, partials, out, counters, n_q, n_kv, pos,
-                         max_seq, scale, ra);
+      attn_go<128, ROPE>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv, pos, max_seq, scale,
+                         ra);
       break;
     default:
       if constexpr (!ROPE)
-        attn_go<256, false>(grid, qkv, k_cache, v_cache, partials, out, counters, n_q, n_kv,
-                            pos, max_seq, scale, ra);
+        attn_go<256, false>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv, pos, max_seq, scale,
+                            ra);
       break;
   }
+  attn_merge_kernel<<<dim3(n_q, head_dim / 32), 64, 0, WST_STREAM>>>(
+      (const float *)partials, (uint16_t *)out, n_q, head_dim, nsplit,
+      (const int32_t *)pos, max_seq, ATTN_TILE / head_dim);
 }
 
 extern "C" int32_t wst_attn_partial_floats(int32_t n_q, int32_t head_dim, int32_t max_seq) {
@@ -433,9 +471,6 @@ static wst_status_t attn_check(const void *q, const void *k_cache, const void *v
   return WST_OK;
 }
 
-static unsigned int *attn_counters() {
-  return (unsigned int *)wst_static_scratch(WST_SCRATCH_ATTN, 4096 * sizeof(unsigned int));
-}
 
 extern "C" wst_status_t wst_attn_decode(const void *q, const void *k_cache, const void *v_cache,
                                         void *partials, void *out, int32_t n_q, int32_t n_kv,
@@ -444,11 +479,9 @@ extern "C" wst_status_t wst_attn_decode(const void *q, const void *k_cache, cons
   const wst_status_t st =
       attn_check(q, k_cache, v_cache, partials, out, n_q, n_kv, head_dim, pos, max_seq);
   if (st != WST_OK) return st;
-  unsigned int *counters = attn_counters();
-  if (!counters) return WST_ERR_OOM;
   const RopeArgs ra{nullptr, nullptr, nullptr, nullptr, 0.0f};
-  attn_launch<false>(head_dim, q, (void *)k_cache, (void *)v_cache, partials, out, counters, n_q,
-                     n_kv, pos, max_seq, scale, ra);
+  attn_launch<false>(head_dim, q, (void *)k_cache, (void *)v_cache, partials, out, n_q, n_kv,
+                     pos, max_seq, scale, ra);
   WST_TRY_KERNEL("wst_attn_decode");
   return WST_OK;
 }
@@ -465,12 +498,10 @@ extern "C" wst_status_t wst_attn_decode_fused(void *qkv, void *k_cache, void *v_
   if (st != WST_OK) return st;
   WST_REQUIRE(cos_tab && sin_tab, "wst_attn_decode_fused: null rope table");
   WST_REQUIRE(head_dim <= 128, "wst_attn_decode_fused: head_dim must be 64 or 128");
-  unsigned int *counters = attn_counters();
-  if (!counters) return WST_ERR_OOM;
   const RopeArgs ra{(const float *)cos_tab, (const float *)sin_tab, (const uint16_t *)q_norm_w,
                     (const uint16_t *)k_norm_w, eps};
-  attn_launch<true>(head_dim, qkv, k_cache, v_cache, partials, out, counters, n_q, n_kv, pos,
-                    max_seq, scale, ra);
+  attn_launch<true>(head_dim, qkv, k_cache, v_cache, partials, out, n_q, n_kv, pos, max_seq,
+                    scale, ra);
   WST_TRY_KERNEL("wst_attn_decode_fused");
   return WST_OK;
 }

@@ -34,6 +34,7 @@
 // * Rows wider than GEMV_MAX_G groups fall back to a simple kernel with the f16
 //   formulation (x read from L2).
 #include "common.hpp"
+#include "hier_xq.hpp"
 
 #include <stdlib.h>
 
@@ -122,87 +123,6 @@ __device__ __forceinline__ float slot_sum(float v) {
 
 // ---------------------------------------------------------------- the kernel
 //
-// The activation table. For each group of 32 columns the block holds, in LDS:
-//   L[k][j]  k = 0..3 (8 columns each), j = 0..3: digit j of X_c for the 8
-//            columns c = 8k..8k+7, nibble i <-> column 8k+i (the packed
-//            weights' own nibble order), as signed 4-bit values in [-8, 7]
-//   C8       8 * sum_c X_c
-//   S        sum_c h_c (f32)
-//   sc       2^(e-28), e = f16 exponent field of max_c |h_c| (at least 1)
-// where X_c = rint(h_c / sc) is h in units of sc: |X_c| < 2^14, so X is h to
-// 14 bits of the group's largest value (f16 itself carries 11), exactly for
-// every h_c within 4 binades of that maximum. X_c = sum_j 16^j D_j with
-// balanced digits D_j in [-8, 7]; D_j is hex digit j of X_c + 0x8888, minus 8.
-//
-// One packed word w (8 nibbles q) against digit word j gives, in one
-// v_dot8_i32_i4 on (w xor 0x88888888) = (q - 8 per nibble),
-//     sum_i (q_i - 8) D_j,i
-// and sum_i q_i X_i = sum_j 16^j (that) + 8 sum_i X_i, all exact in int32.
-// A group then contributes  ls * sc * (sum q X)  to the row's d-term and
-// lm * S to its dmin-term:  y = d * sum_g ls_g Q_g - dmin * sum_g lm_g S_g.
-// Per 8 weights: one xor and four dot8 (the f16 route needs nine VALU ops).
-//
-// The table is built from the f16 vector the GEMV multiplies: h itself for the
-// plain form, f16(x * rms * w) for the NORM form (the same bits wst_rmsnorm
-// writes), so every form of a row computes the same value.
-#define XQ_WORDS 20  // 16 digit words + C8, S, sc, pad
-#define NORM_THREADS 512
-
-__device__ __forceinline__ int sdot8(uint32_t a, uint32_t b, int c) {
-  return __builtin_amdgcn_sdot8((int)a, (int)b, c, false);
-}
-// First link of a dot chain: the three-operand form with an inline zero, so no
-// accumulator is cleared by a separate move.
-__device__ __forceinline__ int sdot8z(uint32_t a, uint32_t b) {
-  int r;
-  asm("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-
-// Table entry for one quarter (8 columns, words k = b & 3) of group b >> 2.
-// The four quarters of a group are four adjacent lanes: quad DPP ops combine
-// them, so all lanes of a quad must call this together (valid or not).
-__device__ __forceinline__ void build_xq(const uint16_t h[8], int b, bool valid,
-                                         uint32_t *__restrict__ xgt) {
-  uint32_t mx = 0;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) mx = max(mx, (uint32_t)(h[e] & 0x7FFFu));
-  mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0xB1, 0xF, 0xF, false));
-  mx = max(mx, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4E, 0xF, 0xF, false));
-  int ef = (int)(mx >> 10);
-  ef = ef < 1 ? 1 : (ef > 30 ? 30 : ef);
-  const float inv = __builtin_bit_cast(float, (uint32_t)(127 + 28 - ef) << 23);
-  const float sc = __builtin_bit_cast(float, (uint32_t)(127 - 28 + ef) << 23);
-  uint32_t L[4] = {0, 0, 0, 0};
-  int sx = 0;
-  float sh = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float hv = h2f(h[e]);
-    sh += hv;
-    const int X = (int)__builtin_rintf(hv * inv);
-    sx += X;
-    const uint32_t U = (uint32_t)(X + 0x8888);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) L[j] |= __builtin_amdgcn_ubfe(U, 4 * j, 4) << (4 * e);
-  }
-  sx += __builtin_amdgcn_update_dpp(0, sx, 0xB1, 0xF, 0xF, false);
-  sx += __builtin_amdgcn_update_dpp(0, sx, 0x4E, 0xF, 0xF, false);
-  sh += dpp_f<0xB1>(sh);
-  sh += dpp_f<0x4E>(sh);
-  if (valid) {
-    uint32_t *e = xgt + (size_t)(b >> 2) * XQ_WORDS;
-    const int k = b & 3;
-    *(uint4 *)(e + 4 * k) = make_uint4(L[0] ^ 0x88888888u, L[1] ^ 0x88888888u,
-                                       L[2] ^ 0x88888888u, L[3] ^ 0x88888888u);
-    if (k == 0) {
-      e[16] = (uint32_t)(8 * sx);
-      e[17] = __float_as_uint(sh);
-      e[18] = __float_as_uint(sc);
-    }
-  }
-}
-
 // y for one or two rows (SWIGLU: gate row r and up row r + nunits).
 //
 // NG groups per lane, WPR waves per row (a row's lanes are lr = 0..64*WPR-1,
@@ -219,11 +139,15 @@ __device__ __forceinline__ void build_xq(const uint16_t h[8], int b, bool valid,
 //         registers (the RMS with the same reduction as wst_rmsnorm), block 0
 //         also stores h when h_out is non-null. Requires NT == NORM_THREADS.
 // SWIGLU: nunits is the intermediate width; the unit writes f16(silu(g) * u).
+//
+// qw, si, xin and norm_w are deliberately not __restrict__: loads through
+// restrict-const pointers count as invariant, and the compiler then issues
+// the weight loads ahead of the activation loads.
 template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU>
 __global__ __launch_bounds__(NT) void gemv_hier_kernel(
-    const uint4 *__restrict__ qw, const uint8_t *__restrict__ si,
-    const uint32_t *__restrict__ sb, const void *__restrict__ xin,
-    const uint16_t *__restrict__ norm_w, float eps, uint16_t *__restrict__ h_out,
+    const uint4 *qw, const uint8_t *si,
+    const uint32_t *__restrict__ sb, const void *xin,
+    const uint16_t *norm_w, float eps, uint16_t *__restrict__ h_out,
     const uint16_t *__restrict__ bias, void *__restrict__ yout, int in_f, int nunits,
     int accum) {
   static_assert(!NORM || NT == NORM_THREADS, "the RMS reduction order assumes 512 threads");
@@ -244,29 +168,28 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   float xf[NORM ? XB : 1][8];
   uint4 xh[NORM ? 1 : XB];
   uint4 nwv[NORM ? XB : 1];
+  // Every load below is unconditional (indices clamped, values masked): the
+  // code stays straight-line, so the compiler counts the loads in flight and
+  // waits for exactly the ones it needs (a load under a branch is followed by
+  // a wait for everything outstanding).
 #pragma unroll
   for (int i = 0; i < XB; ++i) {
     const int b = tid + NT * i;
-    if (b < NB8) {
-      if constexpr (NORM) {
-        const float4 *xv = (const float4 *)((const float *)xin + (size_t)b * 8);
-        const float4 a = xv[0], c = xv[1];
-        xf[i][0] = a.x; xf[i][1] = a.y; xf[i][2] = a.z; xf[i][3] = a.w;
-        xf[i][4] = c.x; xf[i][5] = c.y; xf[i][6] = c.z; xf[i][7] = c.w;
-        nwv[i] = *(const uint4 *)(norm_w + (size_t)b * 8);
-      } else {
-        xh[i] = *(const uint4 *)((const uint16_t *)xin + (size_t)b * 8);
-      }
+    if constexpr (NORM) {
+      const int bc = min(b, NB8 - 1);
+      const float4 *xv = (const float4 *)((const float *)xin + (size_t)bc * 8);
+      const float4 a = xv[0], c = xv[1];
+      xf[i][0] = a.x; xf[i][1] = a.y; xf[i][2] = a.z; xf[i][3] = a.w;
+      xf[i][4] = c.x; xf[i][5] = c.y; xf[i][6] = c.z; xf[i][7] = c.w;
+      nwv[i] = *(const uint4 *)(norm_w + (size_t)bc * 8);
     } else {
-      if constexpr (NORM) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xf[i][e] = 0.0f;
-        nwv[i] = make_uint4(0, 0, 0, 0);
-      } else {
-        xh[i] = make_uint4(0, 0, 0, 0);
-      }
+      xh[i] = *(const uint4 *)((const uint16_t *)xin + (size_t)min(b, NB8 - 1) * 8);
     }
   }
+
+  // The activation loads are issued before the weight loads (a wave's loads
+  // return in order, so the table waits only for them); the non-restrict
+  // pointers keep the compiler from hoisting the weights above them.
 
   // 2. the first unit's packed bytes
   const int stride = gridDim.x * RPB;
@@ -274,36 +197,36 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   uint4 wq[NR][NG];
   uint32_t idx[NR][NG];
   uint32_t sbv[NR];
-  auto load_unit = [&](int row) {
+  auto load_unit = [&](int row) {  // row clamped: past the end loads are unused
+    const int rc = min(row, nunits - 1);
 #pragma unroll
     for (int k = 0; k < NR; ++k) {
-      const int r = row + k * nunits;
+      const int r = rc + k * nunits;
       sbv[k] = sb[r];
       const uint4 *qr = qw + (size_t)r * G;
       const uint8_t *sr = si + (size_t)r * G;
 #pragma unroll
       for (int j = 0; j < NG; ++j) {
-        const int g = lr + j * LPR;
-        if (g < G) {
-          wq[k][j] = ld_stream16(qr + g);
-          idx[k][j] = sr[g];
-        } else {
-          wq[k][j] = make_uint4(0, 0, 0, 0);
-          idx[k][j] = 0;
-        }
+        const int g = min(lr + j * LPR, G - 1);  // lanes past G compute nothing
+        wq[k][j] = ld_stream16(qr + g);
+        idx[k][j] = sr[g];
       }
     }
   };
-  if (base + rs < nunits) load_unit(base + rs);
+  load_unit(base + rs);
 
   // 3. the RMS scale (rms_scale512's order: thread t, blocks t, t+512, ...)
   float s = 1.0f;
   if constexpr (NORM) {
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < XB; ++i)
+    for (int i = 0; i < XB; ++i) {
+      if (tid + NT * i >= NB8)  // clamped duplicates contribute nothing
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[i][e] = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc = fmaf(xf[i][e], xf[i][e], acc);
+    }
     s = 1.0f / sqrtf(block_sum(acc, bred) / (float)in_f + eps);
   }
 
@@ -337,8 +260,20 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
 
   // 5. rows. The trip count is the same for every wave of the block (the
   // WPR > 1 reduction synchronises the block).
-  for (int it = 0; base < nunits; base += stride, ++it) {
+  // Every block has at least one unit (the launch sizes the grid so), and a
+  // do-while keeps the first unit's loads where they are issued: under a
+  // `base < nunits` guard the compiler would move them past the barrier.
+  int it = 0;
+  do {
     const int row = base + rs;
+    // The epilogue's operands are fetched now, ahead of the next unit's weight
+    // loads, so that waiting for them later does not wait for those too.
+    float yv = 0.0f, bv = 0.0f;
+    if constexpr (!SWIGLU) {
+      const int rowc = min(row, nunits - 1);
+      yv = ((const float *)yout)[rowc];
+      bv = h2f((bias ? bias : (const uint16_t *)sb)[rowc]);  // sb: any readable row
+    }
     float as[NR], am[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) as[k] = am[k] = 0.0f;
@@ -378,7 +313,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       lv[k] = d * as[k] - dm * am[k];
     }
     // The next unit's loads go out before this one's reductions and stores.
-    if (base + stride + rs < nunits) load_unit(base + stride + rs);
+    load_unit(base + stride + rs);
     float part[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) part[k] = wave_sum(lv[k]);
@@ -403,12 +338,13 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
         ((uint16_t *)yout)[row] = f2h(g / (1.0f + __expf(-g)) * up);
       } else {
         float v = part[0];
-        if (bias) v += h2f(bias[row]);
-        float *y = (float *)yout;
-        y[row] = accum ? y[row] + v : v;
+        if (bias) v += bv;
+        ((float *)yout)[row] = accum ? yv + v : v;
       }
     }
-  }
+    base += stride;
+    ++it;
+  } while (base < nunits);
 }
 
 // Fallback for rows wider than GEMV_MAX_G groups: x is re-read from L2 per
@@ -550,6 +486,7 @@ static void launch_q(const HierArgs &a) {
 // threads). NORM forms use 512 threads (their RMS order); plain forms with
 // long rows use 1024 so a CU builds its table once.
 #define GEMV_MAX_G 1280  // groups per row handled by the table kernel
+
 template <bool NORM, bool SWIGLU>
 static bool hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
