@@ -143,7 +143,10 @@ __device__ __forceinline__ float slot_sum(float v) {
 // qw, si, xin and norm_w are deliberately not __restrict__: loads through
 // restrict-const pointers count as invariant, and the compiler then issues
 // the weight loads ahead of the activation loads.
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU>
+//
+// PD: units in flight per row slot (1: the next unit's loads are issued after
+// the current unit's compute; 2: one more unit is always in flight).
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD>
 __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     const uint4 *qw, const uint8_t *si,
     const uint32_t *__restrict__ sb, const void *xin,
@@ -191,29 +194,33 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   // return in order, so the table waits only for them); the non-restrict
   // pointers keep the compiler from hoisting the weights above them.
 
-  // 2. the first unit's packed bytes
+  // 2. the first unit's packed bytes (with PD == 2, the second unit's too)
   const int stride = gridDim.x * RPB;
   int base = blockIdx.x * RPB;
-  uint4 wq[NR][NG];
-  uint32_t idx[NR][NG];
-  uint32_t sbv[NR];
-  auto load_unit = [&](int row) {  // row clamped: past the end loads are unused
+  struct Buf {
+    uint4 wq[NR][NG];
+    uint32_t idx[NR][NG];
+    uint32_t sbv[NR];
+  };
+  Buf b0, b1;
+  auto load_unit = [&](Buf &B, int row) {  // row clamped: past the end loads are unused
     const int rc = min(row, nunits - 1);
 #pragma unroll
     for (int k = 0; k < NR; ++k) {
       const int r = rc + k * nunits;
-      sbv[k] = sb[r];
+      B.sbv[k] = sb[r];
       const uint4 *qr = qw + (size_t)r * G;
       const uint8_t *sr = si + (size_t)r * G;
 #pragma unroll
       for (int j = 0; j < NG; ++j) {
         const int g = min(lr + j * LPR, G - 1);  // lanes past G compute nothing
-        wq[k][j] = ld_stream16(qr + g);
-        idx[k][j] = sr[g];
+        B.wq[k][j] = ld_stream16(qr + g);
+        B.idx[k][j] = sr[g];
       }
     }
   };
-  load_unit(base + rs);
+  load_unit(b0, base + rs);
+  if constexpr (PD == 2) load_unit(b1, base + stride + rs);
 
   // 3. the RMS scale (rms_scale512's order: thread t, blocks t, t+512, ...)
   float s = 1.0f;
@@ -264,7 +271,9 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   // do-while keeps the first unit's loads where they are issued: under a
   // `base < nunits` guard the compiler would move them past the barrier.
   int it = 0;
-  do {
+  // One unit from B; B is then refilled with the unit PD strides ahead, issued
+  // after the compute and before the reductions and stores.
+  auto process = [&](Buf &B) {
     const int row = base + rs;
     // The epilogue's operands are fetched now, ahead of the next unit's weight
     // loads, so that waiting for them later does not wait for those too.
@@ -288,7 +297,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       const float S = __uint_as_float(e[17]), sc = __uint_as_float(e[18]);
 #pragma unroll
       for (int k = 0; k < NR; ++k) {
-        const uint4 p = wq[k][j];
+        const uint4 p = B.wq[k][j];
         const uint32_t w0 = p.x ^ 0x88888888u, w1 = p.y ^ 0x88888888u;
         const uint32_t w2 = p.z ^ 0x88888888u, w3 = p.w ^ 0x88888888u;
         int a0 = sdot8(w0, l0.x, c8), a1 = sdot8z(w0, l0.y);
@@ -300,7 +309,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
         a0 = sdot8(w3, l3.x, a0); a1 = sdot8(w3, l3.y, a1);
         a2 = sdot8(w3, l3.z, a2); a3 = sdot8(w3, l3.w, a3);
         const int t = a0 + (a1 << 4) + (a2 << 8) + (a3 << 12);  // sum_i q_i X_i
-        const uint32_t id = idx[k][j];
+        const uint32_t id = B.idx[k][j];
         as[k] = fmaf((float)(id & 0xFu) * sc, (float)t, as[k]);
         am[k] = fmaf((float)(id >> 4), S, am[k]);
       }
@@ -308,12 +317,11 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     float lv[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) {
-      const float d = h2f((uint16_t)(sbv[k] & 0xFFFFu));
-      const float dm = h2f((uint16_t)(sbv[k] >> 16));
+      const float d = h2f((uint16_t)(B.sbv[k] & 0xFFFFu));
+      const float dm = h2f((uint16_t)(B.sbv[k] >> 16));
       lv[k] = d * as[k] - dm * am[k];
     }
-    // The next unit's loads go out before this one's reductions and stores.
-    load_unit(base + stride + rs);
+    load_unit(B, base + PD * stride + rs);
     float part[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) part[k] = wave_sum(lv[k]);
@@ -344,7 +352,16 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     }
     base += stride;
     ++it;
-  } while (base < nunits);
+  };
+  if constexpr (PD == 1) {
+    do process(b0); while (base < nunits);
+  } else {
+    do {
+      process(b0);
+      if (base >= nunits) break;
+      process(b1);
+    } while (base < nunits);
+  }
 }
 
 // Fallback for rows wider than GEMV_MAX_G groups: x is re-read from L2 per
@@ -455,9 +472,22 @@ struct HierArgs {
   int in_f, nunits, accum;
 };
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU>
-static void launch_q(const HierArgs &a) {
-  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU>;
+// Units in flight per row slot. Measured on the 7B shapes: a second buffer
+// helps only when a slot streams many units (the head, ~37 per slot); for the
+// block GEMVs (1 to 5 units per slot) the extra up-front loads cost more than
+// they hide. WST_GEMV_PD=1 or 2 forces one choice.
+static int gemv_pd_override() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("WST_GEMV_PD");
+    v = e ? atoi(e) : 0;
+  }
+  return v;
+}
+
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD>
+static void launch_pd(const HierArgs &a) {
+  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD>;
   const size_t lds = (size_t)(a.in_f / HGROUP) * XQ_WORDS * 4;
   // Resident blocks per CU for this instance and LDS size, queried once.
   static thread_local size_t q_lds = (size_t)-1;
@@ -480,6 +510,17 @@ static void launch_q(const HierArgs &a) {
       (const uint4 *)a.qw, (const uint8_t *)a.si, (const uint32_t *)a.sb, a.x,
       (const uint16_t *)a.norm_w, a.eps, (uint16_t *)a.h_out, (const uint16_t *)a.bias, a.y,
       a.in_f, a.nunits, a.accum);
+}
+
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU>
+static void launch_q(const HierArgs &a) {
+  int pd = gemv_pd_override();
+  if (pd != 1 && pd != 2) {
+    const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR);
+    pd = a.nunits >= 8 * slots ? 2 : 1;
+  }
+  if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1>(a);
+  else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2>(a);
 }
 
 // in_f -> (groups per lane, waves per row, activation blocks per thread,
