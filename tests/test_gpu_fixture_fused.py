@@ -173,11 +173,10 @@ def test_argmax_advance(orc, wk):
     v = np.random.default_rng(3).standard_normal(151936).astype(np.float32)
     idx = wk.DeviceBuffer(1, np.int32)
     pos = wk.DeviceCursor(10)
-    ffi.call("wst_argmax_advance", wk.DeviceBuffer.from_array(v).ptr, idx.ptr, v.size,
-             pos.buf.ptr, 11)
+    vd = wk.DeviceBuffer.from_array(v)  # held: the launches are asynchronous
+    ffi.call("wst_argmax_advance", vd.ptr, idx.ptr, v.size, pos.buf.ptr, 11)
     assert idx.numpy()[0] == orc.argmax(v) and pos.get() == 11
-    ffi.call("wst_argmax_advance", wk.DeviceBuffer.from_array(v).ptr, idx.ptr, v.size,
-             pos.buf.ptr, 11)
+    ffi.call("wst_argmax_advance", vd.ptr, idx.ptr, v.size, pos.buf.ptr, 11)
     assert pos.get() == 11  # saturates at max_seq
 
 

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 
 from conftest import dev_f16, f16
+from whetstone_amd import ffi
 
 pytestmark = pytest.mark.gpu
 
@@ -440,3 +441,48 @@ def test_rescore_refuses_mismatched_shapes(orc, wk):
         rs.apply(wk.DeviceBuffer(vocab + 1, np.float32), dev_f16(wk, f16(orc, x)))
     with pytest.raises(wk.ShapeError):
         rs.apply(wk.DeviceBuffer(vocab, np.float32), wk.DeviceBuffer(hidden - 1, np.float16))
+
+
+@pytest.mark.parametrize("in_f,out_f,n,accum", [(896, 1152, 256, False), (3584, 520, 37, True),
+                                               (4864, 96, 130, False), (64, 9, 1, True)])
+def test_gemm_int4_hier_matches_dequantised_matmul(orc, wk, in_f, out_f, n, accum):
+    """The MFMA chunk GEMM (f16 weight tiles, f32 accumulate) against float64
+    dequant(W) @ x. Each weight is rounded to f16 once, so every output is
+    within 2^-11 * sum_c |w x| of the exact product (bound used with a 2x
+    margin); the bias adds, accumulate adds onto y."""
+    w = orc.fixture_normal(6, 1, in_f * out_f)
+    p, _ = orc.quantize(w, in_f, out_f)
+    lin = wk.QuantLinearHier.from_packed(p)
+    wd = orc.dequantize(p).astype(np.float64)  # [out_f][in_f], the quantiser's dequant
+    xb = f16(orc, orc.fixture_normal(6, 2, n * in_f, 1.5))
+    xf = xb.view(np.float16).astype(np.float64).reshape(n, in_f)
+    bias = f16(orc, orc.fixture_normal(6, 3, out_f, 0.3))
+    y0 = orc.fixture_normal(6, 4, n * out_f, 1.0).reshape(n, out_f)
+    y = wk.DeviceBuffer.from_array(y0.copy())
+    xd, bd = dev_f16(wk, xb), dev_f16(wk, bias)  # held: the launch is asynchronous
+    ffi.call("wst_gemm_int4_hier", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, xd.ptr, bd.ptr, y.ptr,
+             in_f, out_f, n, int(accum))
+    got = y.numpy().reshape(n, out_f).astype(np.float64)
+    want = xf @ wd.T + bias.view(np.float16).astype(np.float64)
+    if accum:
+        want += y0
+    bound = 2.0 * 2.0 ** -11 * (np.abs(xf) @ np.abs(wd).T) + 1e-5 * (1 + np.abs(want))
+    assert np.all(np.abs(got - want) <= bound), float(np.max(np.abs(got - want) / bound))
+
+
+@pytest.mark.parametrize("in_f,out_f,n", [(896, 200, 256), (128, 64, 3), (40, 17, 5)])
+def test_gemm_fp16_matches_matmul(orc, wk, in_f, out_f, n):
+    """wst_gemm_fp16 (MFMA for whole 32-column steps, GEMV loop otherwise):
+    f16 weights and activations are exact inputs, so only f32 accumulation
+    differs from float64."""
+    wb = f16(orc, orc.fixture_normal(7, 1, in_f * out_f, 0.05))
+    xb = f16(orc, orc.fixture_normal(7, 2, n * in_f, 1.0))
+    y = wk.DeviceBuffer(n * out_f, np.float32)
+    wd_, xd = dev_f16(wk, wb), dev_f16(wk, xb)  # held: the launch is asynchronous
+    ffi.call("wst_gemm_fp16", wd_.ptr, xd.ptr, None, y.ptr, in_f, out_f, n, 0)
+    wf = wb.view(np.float16).astype(np.float64).reshape(out_f, in_f)
+    xf = xb.view(np.float16).astype(np.float64).reshape(n, in_f)
+    want = xf @ wf.T
+    got = y.numpy().reshape(n, out_f).astype(np.float64)
+    bound = 1e-5 * (np.abs(xf) @ np.abs(wf).T) + 1e-6
+    assert np.all(np.abs(got - want) <= bound)

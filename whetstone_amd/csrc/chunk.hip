@@ -8,12 +8,12 @@
 
 #define CHUNK_MAX_TOKENS 256
 
-// Implemented in gemm.hip.
-wst_status_t wst_gemm_int4_hier_impl(const void *qw, const void *si, const void *sb,
-                                     const void *x, const void *bias, void *y, int32_t in_f,
-                                     int32_t out_f, int32_t n, int32_t accum);
-
 extern "C" int32_t wst_chunk_max_tokens(void) { return CHUNK_MAX_TOKENS; }
+
+// Implemented in gemm.hip (MFMA).
+wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void *sb,
+                           const void *x, const void *bias, void *y, int32_t in_f, int32_t out_f,
+                           int32_t n, int32_t accum);
 
 extern "C" wst_status_t wst_gemm_int4_hier(const void *qw, const void *si, const void *sb,
                                            const void *x, const void *bias, void *y,
@@ -22,7 +22,11 @@ extern "C" wst_status_t wst_gemm_int4_hier(const void *qw, const void *si, const
   WST_REQUIRE(qw && si && sb && x && y, "wst_gemm_int4_hier: null pointer");
   WST_REQUIRE(in_f > 0 && out_f > 0 && n > 0, "wst_gemm_int4_hier: non-positive dimension");
   WST_REQUIRE(in_f % 32 == 0, "wst_gemm_int4_hier: in_features must be a multiple of 32");
-  return wst_gemm_int4_hier_impl(qw, si, sb, x, bias, y, in_f, out_f, n, accum);
+  WST_REQUIRE(!(((uintptr_t)qw | (uintptr_t)x) & 15u),
+              "wst_gemm_int4_hier: qw and x must be 16-byte aligned");
+  wst_gemm_mfma(true, qw, si, sb, x, bias, y, in_f, out_f, n, accum);
+  WST_TRY_KERNEL("wst_gemm_int4_hier");
+  return WST_OK;
 }
 
 extern "C" wst_status_t wst_gemm_fp16(const void *w, const void *x, const void *bias, void *y,
@@ -30,7 +34,12 @@ extern "C" wst_status_t wst_gemm_fp16(const void *w, const void *x, const void *
   WST_REQUIRE(w && x && y, "wst_gemm_fp16: null pointer");
   WST_REQUIRE(in_f > 0 && out_f > 0 && n > 0, "wst_gemm_fp16: non-positive dimension");
   WST_REQUIRE(in_f % 8 == 0, "wst_gemm_fp16: in_features must be a multiple of 8");
-  for (int j = 0; j < n; ++j) {
+  if (in_f % 32 == 0 && !(((uintptr_t)w | (uintptr_t)x) & 15u)) {
+    wst_gemm_mfma(false, w, nullptr, nullptr, x, bias, y, in_f, out_f, n, accum);
+    WST_TRY_KERNEL("wst_gemm_fp16");
+    return WST_OK;
+  }
+  for (int j = 0; j < n; ++j) {  // widths that are not whole 32-column steps
     const wst_status_t st = wst_gemv_fp16_ex(w, (const uint16_t *)x + (size_t)j * in_f, bias,
                                              (float *)y + (size_t)j * out_f, in_f, out_f, accum);
     if (st != WST_OK) return st;
