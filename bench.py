@@ -20,6 +20,11 @@ The line printed carries:
   cpu_check  the GPU's first-step logits and tokens against that CPU run
 
     python bench.py [--steps 256] [--warmup 8] [--config 3|2] [--cpu-seconds 12]
+
+`--config 4` instead measures the chunked prefill (0.5B shape with QK-norm and
+the int4 head rescored from an fp16 copy, top-32): a 4096-token seeded prompt
+in 256-token chunks through the MFMA GEMMs, then 128 greedy decode steps, and
+prints a line of its own (prefill tok/s and achieved TFLOP/s, decode tok/s).
 """
 import argparse
 import json
@@ -37,13 +42,13 @@ METRIC = "batch=1 decode tok/s + achieved HBM GB/s (% of 8 TB/s), Qwen2.5-0.5B/7
 HBM_PEAK_GBS = 8000.0
 KV_SEED, WEIGHT_SEED, PROMPT_SEED = 2, 0, 1
 TIMED_STAGES = ["qkv", "attn", "o", "gate_up", "down", "head"]
-KERNEL_NAMES = {  # kernel each stage launches in the fused step (rocprof names)
-    "qkv": "gemv_hier_kernel<..., NORM=true, SWIGLU=false>",
-    "attn": "attn_decode_kernel<LP, ROPE=true>",
-    "o": "gemv_hier_kernel<..., NORM=false, SWIGLU=false>",
-    "gate_up": "gemv_hier_kernel<..., NORM=true, SWIGLU=true>",
-    "down": "gemv_hier_kernel<..., NORM=false, SWIGLU=false>",
-    "head": "gemv_hier_kernel<..., NORM=true, SWIGLU=false>",
+KERNEL_NAMES = {  # kernels each stage launches in the fused step (rocprof names)
+    "qkv": "gemv_hier_kernel<NG, WPR, XB, 512, NORM=true, SWIGLU=false, PD>",
+    "attn": "attn_decode_kernel<HD, ROPE=true> + attn_merge_kernel",
+    "o": "gemv_hier_kernel<NG, WPR, XB, NT, NORM=false, SWIGLU=false, PD>",
+    "gate_up": "gemv_hier_kernel<NG, WPR, XB, 512, NORM=true, SWIGLU=true, PD>",
+    "down": "gemv_hier_kernel<NG, WPR, XB, NT, NORM=false, SWIGLU=false, PD>",
+    "head": "gemv_hier_kernel<NG, WPR, XB, 512, NORM=true, SWIGLU=false, PD>",
 }
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.md"
 
@@ -57,7 +62,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=256)
     p.add_argument("--warmup", type=int, default=8)
-    p.add_argument("--config", type=int, default=3, choices=(2, 3))
+    p.add_argument("--config", type=int, default=3, choices=(2, 3, 4))
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline budget (tokens are added until it is spent)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -218,6 +223,64 @@ def cpu_leg(g, cfg, ctx0, first_token, gpu_tokens, gpu_logits0, budget_s, same_c
     return base, check
 
 
+def prefill_bench(E, wk, n_new: int) -> None:
+    """Config 4: chunked prefill of 4096 tokens (256 per chunk), then n_new
+    graph decode steps (none, and no graph capture, for n_new = 0)."""
+    cfg = dict(E.QWEN05B, qk_norm=1, rescore_k=32)
+    n_prompt, chunk = 4096, 256
+    g = E.Model(cfg, seed=WEIGHT_SEED)
+    eng = E.Engine(g, n_prompt + n_new + 8)
+    ids = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt).astype(np.int32)
+    eng.prefill(ids[:chunk], chunked=True)  # warm-up (kernels, scratch), then rewind
+    eng.set_pos(0)
+    wk.synchronize()
+    log(f"prefill {n_prompt} tokens in {chunk}-token chunks")
+    t0 = time.perf_counter()
+    eng.prefill(ids, chunked=True)
+    wk.synchronize()
+    dt_p = time.perf_counter() - t0
+    # FLOPs: every layer GEMM on every token (2 per weight), the causal
+    # attention (q.k and p.v: 2 * 2 * head_dim per (head, cached position)),
+    # and the head on the last token only.
+    H, I, hd, nq, nkv, L = (cfg[k] for k in ("hidden", "inter", "head_dim", "n_q", "n_kv",
+                                               "n_layers"))
+    w_layer = H * (nq + 2 * nkv) * hd + nq * hd * H + H * 2 * I + I * H
+    attn = 2 * 2 * hd * nq * n_prompt * (n_prompt + 1) // 2
+    flops = L * (2 * w_layer * n_prompt + attn) + 2 * cfg["vocab"] * H
+    dt_d = None
+    if n_new > 0:
+        log("capturing the decode graph")
+        eng.capture_graph()
+        for _ in range(8):
+            eng.step()
+            eng.token()
+        eng.set_pos(n_prompt)
+        wk.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n_new):
+            eng.step()
+            eng.token()
+        wk.synchronize()
+        dt_d = time.perf_counter() - t0
+    line = {
+        "metric": "chunked prefill tok/s (config 4)", "value": round(n_prompt / dt_p, 1),
+        "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "dtype": "int4xf16->f32",
+        "data": "synthetic (seeded N(0,0.02) weights packed to int4-hier-g32 on the device; "
+                "seeded random prompt)",
+        "config": {"workload": f"config 4: Qwen2.5-0.5B-shape (QK-norm, head rescore top-32) "
+                               f"chunked prefill of {n_prompt} tokens in {chunk}-token chunks, "
+                               f"then {n_new} greedy decode steps",
+                   "prefill_ms": round(dt_p * 1e3, 2),
+                   "prefill_tflops": round(flops / dt_p / 1e12, 2),
+                   "prefill_flops": flops,
+                   "decode_steps": n_new,
+                   "decode_tok_s": round(n_new / dt_d, 1) if dt_d else None},
+    }
+    eng.close()
+    g.close()
+    print(json.dumps(line), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -230,10 +293,14 @@ def main():
     if a.copy_probe:
         copy_probe(a.copy_probe)
         return
-    if a.steps <= 0 or a.warmup < 0:
-        sys.exit("bench.py: --steps must be positive and --warmup non-negative")
+    if (a.steps <= 0 and not (a.config == 4 and a.steps == 0)) or a.warmup < 0:
+        sys.exit("bench.py: --steps must be positive (0 allowed with --config 4: prefill only) "
+                 "and --warmup non-negative")
 
     from whetstone_amd import engine as E, kernels as wk  # raises if not built
+    if a.config == 4:
+        prefill_bench(E, wk, a.steps)
+        return
     cfg = E.QWEN7B if a.config == 3 else E.QWEN05B
     t_gen = time.perf_counter()
     g = E.Model(cfg, seed=WEIGHT_SEED)
