@@ -109,6 +109,15 @@ __device__ __forceinline__ h16x8 lds_h8(const uint16_t *p) {
   return __builtin_bit_cast(h16x8, *(const uint4 *)p);
 }
 
+// Column of position p in row d of the V^T tile: 8-position blocks are
+// permuted by xor with d / 8, so that the 8-byte stores of a wave (16 or more
+// chunks of 8 dims at once) spread over all LDS banks, while every aligned run
+// of 8 positions an MFMA operand reads stays contiguous.
+template <int P>
+__device__ __forceinline__ int vt_col(int d, int p) {
+  return (((p >> 3) ^ ((d >> 3) & (P / 8 - 1))) << 3) | (p & 7);
+}
+
 // q (already scaled) as its f16 hi part and the f16 rounding of the rest.
 __device__ __forceinline__ void store_q(uint16_t *qh, uint16_t *ql, int at, float v) {
   const uint16_t h = f2h(v);
@@ -153,14 +162,17 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
   const uint16_t *vb = v_cache + (size_t)kvh * max_seq * HD;
 
   // ---- phase A: the slice's K and V requests go out first, all at once.
-  constexpr int LD = P * CH / ATTN_THREADS;  // 16-byte chunks per thread per tile (4)
+  // Thread t holds 16-byte chunk ch = t % CH (dims 8ch..8ch+7) of the four
+  // consecutive positions 4 (t / CH) + i.
+  constexpr int LD = P * CH / ATTN_THREADS;
+  static_assert(LD == 4, "four positions per thread");
+  const int lch = tid % CH, lrow = 4 * (tid / CH);
   uint4 kr[LD], vr[LD];
 #pragma unroll
   for (int i = 0; i < LD; ++i) {
-    const int c = tid + i * ATTN_THREADS, row = c / CH, ch = c % CH;
-    const int t = min(t0 + row, seq - 1);  // clamped: unconditional loads stay batched
-    kr[i] = *(const uint4 *)(kb + (size_t)t * HD + ch * 8);
-    vr[i] = *(const uint4 *)(vb + (size_t)t * HD + ch * 8);
+    const int t = min(t0 + lrow + i, seq - 1);  // clamped: unconditional loads stay batched
+    kr[i] = *(const uint4 *)(kb + (size_t)t * HD + lch * 8);
+    vr[i] = *(const uint4 *)(vb + (size_t)t * HD + lch * 8);
   }
 
   // q for the group's heads, pre-scaled (attention.cu:98-101), into LDS.
@@ -228,17 +240,29 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
 
   // Tiles into LDS; rows past the cached positions are zero (their scores are
   // masked, and a zero V row keeps 0 * v finite).
+  uint32_t vw[LD][4];
 #pragma unroll
   for (int i = 0; i < LD; ++i) {
-    const int c = tid + i * ATTN_THREADS, row = c / CH, ch = c % CH;
-    const uint32_t mk = t0 + row < t1 ? 0xFFFFFFFFu : 0u;  // a mask, not a select of
-    const uint4 a = kr[i], b = vr[i];                      // addresses (which spills)
-    *(uint4 *)(ktile + row * S::KS + ch * 8) = make_uint4(a.x & mk, a.y & mk, a.z & mk, a.w & mk);
-    const uint32_t vw[4] = {b.x & mk, b.y & mk, b.z & mk, b.w & mk};
+    const uint32_t mk = t0 + lrow + i < t1 ? 0xFFFFFFFFu : 0u;  // a mask, not a select of
+    const uint4 a = kr[i], b = vr[i];                             // addresses (which spills)
+    *(uint4 *)(ktile + (lrow + i) * S::KS + lch * 8) =
+        make_uint4(a.x & mk, a.y & mk, a.z & mk, a.w & mk);
+    vw[i][0] = b.x & mk;
+    vw[i][1] = b.y & mk;
+    vw[i][2] = b.z & mk;
+    vw[i][3] = b.w & mk;
+  }
+  // V^T: dim d's four positions as one 8-byte store (halves picked by byte
+  // permutes), at the swizzled column of vt_col.
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {  // V^T: dims are rows
-      vtile[(ch * 8 + 2 * e) * S::VS + row] = (uint16_t)(vw[e] & 0xFFFFu);
-      vtile[(ch * 8 + 2 * e + 1) * S::VS + row] = (uint16_t)(vw[e] >> 16);
+  for (int e = 0; e < 4; ++e) {
+#pragma unroll
+    for (int odd = 0; odd < 2; ++odd) {
+      const uint32_t sel = odd ? 0x07060302u : 0x05040100u;
+      const uint32_t lo = __builtin_amdgcn_perm(vw[1][e], vw[0][e], sel);
+      const uint32_t hi = __builtin_amdgcn_perm(vw[3][e], vw[2][e], sel);
+      const int d = lch * 8 + 2 * e + odd;
+      *(uint2 *)(vtile + d * S::VS + vt_col<P>(d, lrow)) = make_uint2(lo, hi);
     }
   }
   if constexpr (ROPE) {
@@ -247,8 +271,8 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
       const int row = pos - t0;
       ktile[row * S::KS + lane] = knew;
       ktile[row * S::KS + lane + HD / 2] = knew2;
-      vtile[lane * S::VS + row] = vnew;
-      vtile[(lane + HD / 2) * S::VS + row] = vnew2;
+      vtile[lane * S::VS + vt_col<P>(lane, row)] = vnew;
+      vtile[(lane + HD / 2) * S::VS + vt_col<P>(lane + HD / 2, row)] = vnew2;
     }
   }
   __syncthreads();
@@ -311,14 +335,14 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
   {
     const int r16 = lane & 15, kq = (lane >> 4) * 8;
     for (int nd = wave; nd < HD / 16; nd += ATTN_WAVES) {
+      const int d = nd * 16 + r16;
       f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
       for (int kk = 0; kk < P; kk += 32) {
-        const h16x8 b = lds_h8(vtile + (nd * 16 + r16) * S::VS + kk + kq);
+        const h16x8 b = lds_h8(vtile + d * S::VS + vt_col<P>(d, kk + kq));
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(ph + r16 * S::PS + kk + kq), b, c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pl + r16 * S::PS + kk + kq), b, c, 0, 0, 0);
       }
-      const int d = nd * 16 + r16;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h = (lane >> 4) * 4 + i;
@@ -410,7 +434,7 @@ static void attn_go(const dim3 grid, const void *qkv, void *k_cache, void *v_cac
                     const RopeArgs &ra) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipFuncSetAttribute((const void *)attn_decode_kernel<HD, ROPE>,
+    (void)hipFuncSetAttribute((const void *)attn_decode_kernel<HD, ROPE>,
                         hipFuncAttributeMaxDynamicSharedMemorySize, AttnShape<HD>::LDS);
     attr_set = true;
   }
