@@ -290,7 +290,12 @@ def test_attention_over_two_positions_matches_explicit_softmax(orc, wk):
 
 @pytest.mark.parametrize("n_q,n_kv,hd,max_seq,pos", [(14, 2, 64, 1024, 700), (28, 4, 128, 2304, 2047),
                                                      (8, 8, 128, 64, 63), (7, 1, 64, 5000, 4999),
-                                                     (4, 2, 256, 300, 150)])
+                                                     (4, 2, 256, 300, 150),
+                                                     # more than two merge runs (> 32 slices)
+                                                     (28, 4, 128, 4608, 4500),
+                                                     (14, 2, 64, 9000, 8999),
+                                                     # few live slices of many
+                                                     (28, 4, 128, 8192, 300)])
 def test_attention_matches_oracle_on_random_caches(orc, wk, n_q, n_kv, hd, max_seq, pos):
     rng = np.random.default_rng(pos)
     kc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))

@@ -362,53 +362,64 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
 //
 // out[h][d] = sum_s e^(m_s - M) acc_s[d] / sum_s e^(m_s - M) l_s with M the
 // largest slice maximum (attention.cu:170-193). One 64-thread block per (head,
-// 32 dims): lane (half, d) combines a contiguous half of the slices in slice
-// order, fetching ATTN_MERGE_BATCH of them per round trip; the two halves are
-// then combined in order.
+// 32 dims): lane (half, d) combines slices half*B .. half*B+B-1 of every run of
+// 2B (B = ATTN_MERGE_BATCH) in slice order, then the two halves are combined.
+// The first run's loads do not wait for the position: they are issued with it
+// (slice indices clamped to the partials' extent) and slices past the cached
+// ones are masked afterwards, so the merge costs one memory round trip, not two.
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ partials,
-                                                        uint16_t *__restrict__ out, int n_q, int hd,
-                                                        int nsplit,
+                                                        uint16_t *__restrict__ out, int n_q,
+                                                        int hd, int nsplit,
                                                         const int32_t *__restrict__ pos_dev,
                                                         int max_seq, int P) {
+  constexpr int B = ATTN_MERGE_BATCH;
   __shared__ float hx[32][3];
   const int h = blockIdx.x, d0 = blockIdx.y * 32, lane = threadIdx.x;
   const int half = lane >> 5, d = d0 + (lane & 31);
-  const int seq = min(max(*pos_dev, 0) + 1, max_seq);
-  const int nactive = (seq + P - 1) / P;
   const float *pacc = partials;
   const float *pml = partials + (size_t)n_q * nsplit * hd;
-  const int run = (nactive + 1) / 2;
-  const int s0 = half * run, s1 = min(s0 + run, nactive);
   const size_t row0 = (size_t)h * nsplit;
+  const int pos = *pos_dev;
   float M = -INFINITY, den = 0.0f, a = 0.0f;
-  for (int c0 = s0; c0 < s1; c0 += ATTN_MERGE_BATCH) {
-    float ms[ATTN_MERGE_BATCH], ls[ATTN_MERGE_BATCH], vs[ATTN_MERGE_BATCH];
-    // Unconditional loads (a clamped slice index) so that all of them are in
-    // flight together.
+  int c = 0, nactive = 1;
+  do {
+    float ms[B], ls[B], vs[B];
 #pragma unroll
-    for (int i = 0; i < ATTN_MERGE_BATCH; ++i) {
-      const int sl = c0 + i;
-      const size_t r = row0 + (sl < s1 ? sl : s1 - 1);
+    for (int i = 0; i < B; ++i) {
+      const size_t r = row0 + min(c + half * B + i, nsplit - 1);
       const float2 mlv = *(const float2 *)(pml + r * 2);
-      ms[i] = sl < s1 ? mlv.x : -INFINITY;
+      ms[i] = mlv.x;
       ls[i] = mlv.y;
       vs[i] = pacc[r * hd + d];
     }
+    const int seq = min(max(pos, 0) + 1, max_seq);
+    nactive = (seq + P - 1) / P;
+    // Slices past the cached positions hold stale partials: replaced, not
+    // multiplied by zero, so nothing non-finite can enter.
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const bool live = c + half * B + i < nactive;
+      ms[i] = live ? ms[i] : -INFINITY;
+      ls[i] = live ? ls[i] : 0.0f;
+      vs[i] = live ? vs[i] : 0.0f;
+    }
     float Mn = M;
 #pragma unroll
-    for (int i = 0; i < ATTN_MERGE_BATCH; ++i) Mn = fmaxf(Mn, ms[i]);
-    const float fo = (M == -INFINITY) ? 0.0f : __expf(M - Mn);
-    a *= fo;
-    den *= fo;
+    for (int i = 0; i < B; ++i) Mn = fmaxf(Mn, ms[i]);
+    if (Mn != -INFINITY) {  // else nothing live in this run for this half
+      const float fo = (M == -INFINITY) ? 0.0f : __expf(M - Mn);
+      a *= fo;
+      den *= fo;
 #pragma unroll
-    for (int i = 0; i < ATTN_MERGE_BATCH; ++i) {
-      // slices past the run carry m = -inf: f = 0 adds exact zeros
-      const float f = (ms[i] == -INFINITY) ? 0.0f : __expf(ms[i] - Mn);
-      a = fmaf(vs[i], f, a);
-      den = fmaf(ls[i], f, den);
+      for (int i = 0; i < B; ++i) {
+        const float f = (ms[i] == -INFINITY) ? 0.0f : __expf(ms[i] - Mn);
+        a = fmaf(vs[i], f, a);
+        den = fmaf(ls[i], f, den);
+      }
+      M = Mn;
     }
-    M = Mn;
-  }
+    c += 2 * B;
+  } while (c < nactive);
   if (half == 1) {
     hx[lane & 31][0] = M;
     hx[lane & 31][1] = den;
