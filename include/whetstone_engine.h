@@ -37,6 +37,11 @@ typedef struct {
   int32_t rescore_k; /* > 0: keep an f16 head copy and rescore the top k */
   float eps;
   double rope_theta;
+  /* RoPE frequency schedule (decode.rs RopeScaling): 0 none, 1 Llama-3
+   * piecewise (factor, low/high frequency factors, original context). */
+  int32_t rope_llama3;
+  int32_t rope_orig_max;
+  double rope_factor, rope_low_freq, rope_high_freq;
 } wse_config_t;
 
 typedef struct wse_model wse_model_t;
@@ -71,8 +76,40 @@ void wse_model_free(wse_model_t *m);
  * "L<l>.o", "L<l>.gate_up", "L<l>.down". */
 wst_status_t wse_model_tensor(wse_model_t *m, const char *name, void **qw, void **si, void **sb,
                               int64_t *in_f, int64_t *out_f);
+/* Device pointer and length of an f16 tensor of the model: "final_norm",
+ * "rescore" (the head's f16 copy), "embed16" / "lm_head16" (dense tables),
+ * "L<l>.in_norm", "L<l>.post_norm", "L<l>.qkv_bias", "L<l>.q_norm",
+ * "L<l>.k_norm". WST_ERR_SHAPE when the model has no such tensor. */
+wst_status_t wse_model_vector(wse_model_t *m, const char *name, void **ptr, int64_t *n);
 /* Weight bytes a decode step streams (packed matrices + norms + biases). */
 uint64_t wse_model_weight_bytes(const wse_model_t *m);
+/* The model's dimensions and flags as built or loaded. */
+wst_status_t wse_model_config(const wse_model_t *m, wse_config_t *out);
+
+/* ----------------------------------------------------------- .wstone files
+ * The converted-model container (crates/whetstone-quant/src/format.rs,
+ * docs/FORMAT.md). Refusals return WST_ERR_INVALID_ARG (format, config) or
+ * WST_ERR_SHAPE with the reason in wse_last_error(). */
+
+/* The container's 64-bit hash (format.rs:225-232): FNV-1a's offset basis and
+ * xor-then-multiply, with the multiplier 0x1000000001B3 the reference uses. */
+uint64_t wse_fnv1a(const void *bytes, size_t n);
+/* Parses and validates a file's header as format.rs:427-516 does: magic,
+ * version, header hash, the JSON, every blob range inside the file and
+ * 256-byte aligned, and the blobs each kind requires. verify != 0 also checks
+ * every payload hash (format.rs:518-547). Host only; needs no GPU. */
+wst_status_t wse_wstone_check(const char *path, int32_t verify, int32_t *n_tensors);
+/* The embedded config.json parsed and validated (config.rs:26-262: defaults,
+ * architecture whitelist, MoE and unsupported RoPE scaling refused). Host only. */
+wst_status_t wse_wstone_config(const char *path, wse_config_t *out);
+/* The same parse and validation of a config.json text. Host only. */
+wst_status_t wse_config_from_json(const char *json, wse_config_t *out);
+/* Loads a file into a device model (model.rs:454-638): q|k|v and gate|up
+ * fused by row append, q/k/v biases fused with zero fill, QK-norm gains when
+ * present (both or neither), embedding and head as int4_hier_g32 or f16.
+ * rescore_k: < 0 uses 64 when the file carries the head's ".rescore" f16 copy
+ * (model.rs:814), 0 disables the rescore, > 0 sets k. */
+wst_status_t wse_model_load_wstone(const char *path, int32_t rescore_k, wse_model_t **out);
 
 wst_status_t wse_engine_create(wse_model_t *m, int32_t max_seq, int32_t step_mode,
                                wse_engine_t **out);

@@ -21,6 +21,9 @@
  *   head ladder         reference rescore tests restated (rescore_kernels.rs)
  *   forward (textbook)  HF transformers Qwen2 in float64 on the same weights
  *   forward (mirrored)  textbook forward within fp16 tolerance
+ *   dense f16 tables    (mirrored step) tables set to the f16 rounding of the
+ *                       dequantised int4 ones give the int4 logits within f16
+ *                       noise; the f16 GEMV by numpy float64 matmul
  */
 #include "oracle.h"
 
@@ -568,6 +571,10 @@ struct orc_model {
   hmat_t embed, lm_head; /* lm_head.qw == NULL when tied */
   uint16_t *final_norm;
   uint16_t *rescore; /* [V][H] fp16 copy of the head, or NULL */
+  /* Dense f16 [V][H] embedding / output projection (a converted model's fp16
+   * tables, model.rs Embedding::Fp16 and DeviceLinear::Fp16), or NULL. Used by
+   * the mirrored step only. */
+  uint16_t *embed16, *head16;
   layer_t *layers;
 };
 
@@ -685,6 +692,8 @@ void orc_model_free(orc_model_t *m) {
   hmat_free(&m->lm_head);
   free(m->final_norm);
   free(m->rescore);
+  free(m->embed16);
+  free(m->head16);
   for (int l = 0; l < m->c.n_layers; ++l) {
     layer_t *L = &m->layers[l];
     hmat_free(&L->qkv);
@@ -725,6 +734,21 @@ int orc_model_tensor(orc_model_t *m, const char *name, const uint32_t **qw,
   *sb = h->sb;
   *in_f = h->in_f;
   *out_f = h->out_f;
+  return 0;
+}
+
+/* Replaces the embedding ("embed") or the output projection ("head") by a dense
+ * f16 [vocab][hidden] table (copied). With a tied model the embedding table
+ * also serves as the head. Returns 0, or -1 for an unknown name. */
+int orc_model_set_dense(orc_model_t *m, const char *which, const uint16_t *table) {
+  const size_t n = (size_t)m->c.vocab * (size_t)m->c.hidden;
+  uint16_t **dst = strcmp(which, "embed") == 0 ? &m->embed16
+                   : strcmp(which, "head") == 0 ? &m->head16
+                                                : NULL;
+  if (!dst) return -1;
+  free(*dst);
+  *dst = (uint16_t *)malloc(n * 2);
+  memcpy(*dst, table, n * 2);
   return 0;
 }
 
@@ -884,7 +908,11 @@ int32_t orc_step(orc_state_t *s, int32_t token, float *logits_out) {
     uint16_t *attn = (uint16_t *)malloc((size_t)nq * hd * 2);
     float *gu = (float *)malloc((size_t)2 * I * 4);
     uint16_t *act = (uint16_t *)malloc((size_t)I * 2);
-    orc_dequantize_row(m->embed.qw, m->embed.si, m->embed.sb, H, token, x);
+    if (m->embed16) {  /* decode.cu:259-268: the f16 row widened to f32 */
+      for (int i = 0; i < H; ++i) x[i] = h2f(m->embed16[(size_t)token * H + i]);
+    } else {
+      orc_dequantize_row(m->embed.qw, m->embed.si, m->embed.sb, H, token, x);
+    }
     for (int l = 0; l < c->n_layers; ++l) {
       const layer_t *L = &m->layers[l];
       orc_rmsnorm(x, L->in_norm, h, H, c->eps);
@@ -899,7 +927,11 @@ int32_t orc_step(orc_state_t *s, int32_t token, float *logits_out) {
       orc_gemv_int4_hier(L->down.qw, L->down.si, L->down.sb, act, NULL, x, I, H, 1);
     }
     orc_rmsnorm(x, m->final_norm, h, H, c->eps);
-    orc_gemv_int4_hier(head->qw, head->si, head->sb, h, NULL, logits, H, V, 0);
+    const uint16_t *head16 = c->tied ? m->embed16 : m->head16;
+    if (head16)
+      orc_gemv_fp16(head16, h, NULL, logits, H, V, 0);
+    else
+      orc_gemv_int4_hier(head->qw, head->si, head->sb, h, NULL, logits, H, V, 0);
     if (m->rescore && c->rescore_k > 0) {
       const int k = c->rescore_k;
       int cap = 16 * k;

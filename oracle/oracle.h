@@ -101,6 +101,7 @@ void orc_model_free(orc_model_t *m);
 int orc_model_tensor(orc_model_t *m, const char *name, const uint32_t **qw,
                      const uint8_t **si, const uint32_t **sb, int64_t *in_f, int64_t *out_f);
 const uint16_t *orc_model_fp16(orc_model_t *m, const char *name, int64_t *n);
+int orc_model_set_dense(orc_model_t *m, const char *which, const uint16_t *table);
 
 /* mode 0: precision-mirrored (f16 at the kernels' narrowing points),
  * mode 1: textbook f64 (no narrowing, f64 KV cache). */

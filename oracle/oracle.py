@@ -87,6 +87,7 @@ def lib():
                                        C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
                                        C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
         "orc_model_fp16": (C.c_void_p, [C.c_void_p, C.c_char_p, C.POINTER(C.c_int64)]),
+        "orc_model_set_dense": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p]),
         "orc_state_new": (C.c_void_p, [C.c_void_p, C.c_int, C.c_int]),
         "orc_state_free": (None, [C.c_void_p]),
         "orc_state_pos": (C.c_int, [C.c_void_p]),
@@ -258,6 +259,14 @@ class Model:
         if not p or n.value == 0:
             return None
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), (n.value,))
+
+    def set_dense(self, which: str, table_bits) -> None:
+        """Dense f16 [vocab][hidden] embedding ("embed") or head ("head")."""
+        t = np.ascontiguousarray(table_bits, np.uint16)
+        if t.size != self.cfg["vocab"] * self.cfg["hidden"]:
+            raise ValueError("table must be [vocab][hidden]")
+        if lib().orc_model_set_dense(self.h, which.encode(), t.ctypes.data) != 0:
+            raise KeyError(which)
 
     def forward_full(self, ids) -> np.ndarray:
         ids = np.ascontiguousarray(ids, np.int32)

@@ -145,3 +145,23 @@ def test_golden_fixture_is_reproduced(orc):
         got.append(nxt)
         nxt, _ = st.step(nxt)
     assert got == gold["tokens"][:6]
+
+
+def test_mirrored_step_with_dense_f16_tables(orc):
+    """Dense f16 embedding / head (a converted model's fp16 tables): set to the
+    f16 rounding of the dequantised int4 tables, the logits stay within f16
+    noise of the int4 run (and differ from it: the dense tables are used)."""
+    for cfg in (TINY, TINY_QK):
+        m, d = orc.Model(cfg, seed=31), orc.Model(cfg, seed=31)
+        emb = orc.f16_bits(orc.dequantize(m.tensor("embed")))
+        d.set_dense("embed", emb)
+        if not cfg["tied"]:
+            d.set_dense("head", orc.f16_bits(orc.dequantize(m.tensor("lm_head"))))
+        a, b = orc.State(m, 16, 0), orc.State(d, 16, 0)
+        for t in _ids(6, cfg["vocab"], 9):
+            _, la = a.step(int(t))
+            _, lb = b.step(int(t))
+            scale = np.sqrt(np.mean(la.astype(np.float64) ** 2))
+            assert np.max(np.abs(la - lb)) < 3e-3 * max(scale, 1.0)
+            assert np.max(np.abs(la - lb)) > 0  # the dense tables are in use
+        a.close(), b.close(), m.close(), d.close()

@@ -13,53 +13,24 @@
 #include <string>
 #include <vector>
 
+#include "engine_internal.hpp"
 #include "whetstone.h"
 #include "whetstone_ext.h"
 
-namespace {
+namespace wse {
 
 thread_local char g_msg[512];
 
-#define TRY(expr)                                  \
-  do {                                             \
-    const wst_status_t _s = (expr);                \
-    if (_s != WST_OK) return _s;                   \
-  } while (0)
-
-// Engine-level refusals carry their message in g_msg (wse_last_error); kernel
-// failures keep theirs in the library's wst_last_error.
 wst_status_t shape_error(const char *fmt, const char *what) {
   snprintf(g_msg, sizeof(g_msg), fmt, what);
   return WST_ERR_SHAPE;
 }
 
-struct Mat {
-  void *qw = nullptr, *si = nullptr, *sb = nullptr;
-  int64_t in_f = 0, out_f = 0;
-  uint64_t bytes() const { return (uint64_t)out_f * (uint64_t)(in_f / 2 + in_f / 32 + 4); }
-};
+}  // namespace wse
 
-struct Layer {
-  Mat qkv, o, gate_up, down;
-  void *qkv_bias = nullptr, *in_norm = nullptr, *post_norm = nullptr;
-  void *q_norm = nullptr, *k_norm = nullptr;
-};
+using namespace wse;
 
-// Device allocations owned by a model or an engine, freed together.
-struct Arena {
-  std::vector<void *> ptrs;
-  wst_status_t alloc(void **out, size_t bytes, bool zero) {
-    *out = nullptr;
-    TRY(wst_malloc(out, bytes));
-    ptrs.push_back(*out);
-    if (zero) TRY(wst_memset(*out, 0, bytes));
-    return WST_OK;
-  }
-  void free_all() {
-    for (void *p : ptrs) wst_free(p);
-    ptrs.clear();
-  }
-};
+namespace {
 
 // Fixture streams, shared with the CPU oracle (oracle/oracle.c).
 enum { ST_Q = 0, ST_K = 1, ST_V = 2, ST_O = 3, ST_GATE = 4, ST_UP = 5, ST_DOWN = 6, ST_QN = 7, ST_KN = 8 };
@@ -67,16 +38,6 @@ inline uint64_t stream_of(int l, int t) { return (uint64_t)l * 16u + (uint64_t)t
 constexpr uint64_t ST_EMBED = 1, ST_HEAD = 2;
 
 }  // namespace
-
-struct wse_model {
-  wse_config_t c{};
-  Mat embed, lm_head;
-  void *final_norm = nullptr;
-  void *rescore = nullptr;  // f16 [vocab][hidden]
-  std::vector<Layer> layers;
-  Arena arena;
-  const Mat &head() const { return c.tied ? embed : lm_head; }
-};
 
 struct wse_engine {
   wse_model *m = nullptr;
@@ -97,13 +58,7 @@ struct wse_engine {
   Arena arena;
 };
 
-extern "C" {
-
-const char *wse_last_error(void) { return g_msg; }
-
-// ------------------------------------------------------------------- model
-
-static wst_status_t alloc_mat(Arena &a, Mat &m, int64_t in_f, int64_t out_f) {
+wst_status_t wse::alloc_mat(Arena &a, Mat &m, int64_t in_f, int64_t out_f) {
   m.in_f = in_f;
   m.out_f = out_f;
   TRY(a.alloc(&m.qw, (size_t)(out_f * in_f / 2), false));
@@ -112,17 +67,7 @@ static wst_status_t alloc_mat(Arena &a, Mat &m, int64_t in_f, int64_t out_f) {
   return WST_OK;
 }
 
-static wst_status_t pack_part(Mat &m, int64_t row0, int64_t rows, uint64_t seed, uint64_t stream) {
-  return wst_fixture_pack_hier(m.qw, m.si, m.sb, m.in_f, row0, rows, seed, stream, 0.02f);
-}
-
-static wst_status_t f16_fill(Arena &a, void **out, size_t n, uint64_t seed, uint64_t stream,
-                             float std_, float offset) {
-  TRY(a.alloc(out, n * 2, false));
-  return wst_fixture_normal_f16(*out, n, seed, stream, 0, std_, offset);
-}
-
-static wst_status_t check_config(const wse_config_t *c) {
+wst_status_t wse::check_config(const wse_config_t *c) {
   if (!c || c->n_layers <= 0 || c->hidden <= 0 || c->n_q <= 0 || c->n_kv <= 0 ||
       c->head_dim <= 0 || c->inter <= 0 || c->vocab <= 0) {
     snprintf(g_msg, sizeof(g_msg), "config: non-positive dimension");
@@ -137,6 +82,24 @@ static wst_status_t check_config(const wse_config_t *c) {
   }
   return WST_OK;
 }
+
+extern "C" {
+
+const char *wse_last_error(void) { return g_msg; }
+
+// ------------------------------------------------------------------- model
+
+
+static wst_status_t pack_part(Mat &m, int64_t row0, int64_t rows, uint64_t seed, uint64_t stream) {
+  return wst_fixture_pack_hier(m.qw, m.si, m.sb, m.in_f, row0, rows, seed, stream, 0.02f);
+}
+
+static wst_status_t f16_fill(Arena &a, void **out, size_t n, uint64_t seed, uint64_t stream,
+                             float std_, float offset) {
+  TRY(a.alloc(out, n * 2, false));
+  return wst_fixture_normal_f16(*out, n, seed, stream, 0, std_, offset);
+}
+
 
 static wst_status_t model_build(wse_model *m, uint64_t seed) {
   const wse_config_t &c = m->c;
@@ -224,6 +187,52 @@ wst_status_t wse_model_tensor(wse_model_t *m, const char *name, void **qw, void 
   return WST_OK;
 }
 
+wst_status_t wse_model_vector(wse_model_t *m, const char *name, void **ptr, int64_t *n) {
+  if (!m || !name || !ptr || !n) return WST_ERR_INVALID_ARG;
+  const wse_config_t &c = m->c;
+  void *p = nullptr;
+  int64_t len = 0;
+  if (!strcmp(name, "final_norm")) {
+    p = m->final_norm;
+    len = c.hidden;
+  } else if (!strcmp(name, "rescore")) {
+    p = m->rescore;
+    len = (int64_t)c.vocab * c.hidden;
+  } else if (!strcmp(name, "embed16")) {
+    p = m->embed.w16;
+    len = (int64_t)c.vocab * c.hidden;
+  } else if (!strcmp(name, "lm_head16")) {
+    p = m->head().w16;
+    len = (int64_t)c.vocab * c.hidden;
+  } else {
+    int l = -1;
+    char what[32] = {0};
+    if (sscanf(name, "L%d.%31s", &l, what) == 2 && l >= 0 && l < c.n_layers) {
+      const Layer &L = m->layers[(size_t)l];
+      if (!strcmp(what, "in_norm")) {
+        p = L.in_norm;
+        len = c.hidden;
+      } else if (!strcmp(what, "post_norm")) {
+        p = L.post_norm;
+        len = c.hidden;
+      } else if (!strcmp(what, "qkv_bias")) {
+        p = L.qkv_bias;
+        len = (int64_t)(c.n_q + 2 * c.n_kv) * c.head_dim;
+      } else if (!strcmp(what, "q_norm")) {
+        p = L.q_norm;
+        len = c.head_dim;
+      } else if (!strcmp(what, "k_norm")) {
+        p = L.k_norm;
+        len = c.head_dim;
+      }
+    }
+  }
+  if (!p) return shape_error("no f16 vector %s in this model", name);
+  *ptr = p;
+  *n = len;
+  return WST_OK;
+}
+
 // config.rs:347-362 (decode_resident) restated for this layout: every packed
 // matrix the step streams, plus norm gains and biases. The embedding-row gather
 // and the rescore copy are excluded, as the reference excludes them.
@@ -241,12 +250,26 @@ uint64_t wse_model_weight_bytes(const wse_model_t *m) {
 // ------------------------------------------------------------------ engine
 
 static wst_status_t rope_table(wse_engine *e) {
-  // decode.rs:95-147 (no scaling): invf = theta^(-j/half) in f64, angle p*invf
-  // in f64, narrowed to f32.
-  const int hd = e->m->c.head_dim, half = hd / 2;
+  // decode.rs:95-147: invf = theta^(-j/half) in f64 (Llama-3 schedule: divided
+  // by factor past the low-frequency wavelength, blended across the band
+  // between), angle p*invf in f64, narrowed to f32.
+  const wse_config_t &c = e->m->c;
+  const int hd = c.head_dim, half = hd / 2;
   std::vector<float> cs((size_t)e->max_seq * half), sn((size_t)e->max_seq * half);
   for (int j = 0; j < half; ++j) {
-    const double invf = pow(e->m->c.rope_theta, -(double)j / (double)half);
+    double invf = pow(c.rope_theta, -(double)j / (double)half);
+    if (c.rope_llama3) {
+      const double orig = (double)c.rope_orig_max;
+      const double low_wl = orig / c.rope_low_freq, high_wl = orig / c.rope_high_freq;
+      const double wavelen = 2.0 * M_PI / invf;
+      if (wavelen > low_wl) {
+        invf /= c.rope_factor;
+      } else if (wavelen > high_wl) {
+        const double smooth =
+            (orig / wavelen - c.rope_low_freq) / (c.rope_high_freq - c.rope_low_freq);
+        invf = (1.0 - smooth) * (invf / c.rope_factor) + smooth * invf;
+      }
+    }
     for (int p = 0; p < e->max_seq; ++p) {
       const double a = (double)p * invf;
       cs[(size_t)p * half + j] = (float)cos(a);
@@ -367,6 +390,32 @@ struct Marks {
 };
 
 // Engine::step_eager (engine.rs:512-572) in either launch sequence.
+// The embedding gather and the output projection: int4-hier or, for models
+// converted with an f16 head (the reference converter's default), dense f16.
+static wst_status_t embed_token(wse_engine *e) {
+  const wse_model &m = *e->m;
+  if (m.embed.dense())
+    return wst_embed_fp16(m.embed.w16, e->token, e->x, m.c.hidden, m.c.vocab);
+  return wst_embed_int4_hier(m.embed.qw, m.embed.si, m.embed.sb, e->token, e->x, m.c.hidden,
+                             m.c.vocab);
+}
+
+// Final RMSNorm of x_last (f32 [H]) into e->h, then logits = head . h.
+static wst_status_t head_logits(wse_engine *e, const void *x_last, bool fused) {
+  const wse_model &m = *e->m;
+  const Mat &head = m.head();
+  const int H = m.c.hidden, V = m.c.vocab;
+  if (head.dense()) {
+    TRY(wst_rmsnorm(x_last, m.final_norm, e->h, H, m.c.eps));
+    return wst_gemv_fp16(head.w16, e->h, e->logits, H, V);
+  }
+  if (fused)
+    return wst_gemv_hier_rmsnorm(head.qw, head.si, head.sb, x_last, m.final_norm, m.c.eps, e->h,
+                                 nullptr, e->logits, H, V, 0);
+  TRY(wst_rmsnorm(x_last, m.final_norm, e->h, H, m.c.eps));
+  return wst_gemv_int4_hier_ex(head.qw, head.si, head.sb, e->h, nullptr, e->logits, H, V, 0);
+}
+
 static wst_status_t step_eager(wse_engine *e, Marks &mk) {
   const wse_model &m = *e->m;
   const wse_config_t &c = m.c;
@@ -375,10 +424,9 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
   const float eps = c.eps;
   const float scale = (float)(1.0 / sqrt((double)hd));
   const bool fused = e->mode == WSE_STEP_FUSED;
-  const Mat &head = m.head();
 
   TRY(mk.mark(-1));
-  TRY(wst_embed_int4_hier(m.embed.qw, m.embed.si, m.embed.sb, e->token, e->x, H, V));
+  TRY(embed_token(e));
   TRY(mk.mark(WSE_STAGE_EMBED));
   for (int l = 0; l < c.n_layers; ++l) {
     const Layer &L = m.layers[(size_t)l];
@@ -415,13 +463,7 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
     TRY(wst_gemv_int4_hier_ex(L.down.qw, L.down.si, L.down.sb, e->act, nullptr, e->x, I, H, 1));
     TRY(mk.mark(WSE_STAGE_DOWN));
   }
-  if (fused) {
-    TRY(wst_gemv_hier_rmsnorm(head.qw, head.si, head.sb, e->x, m.final_norm, eps, e->h, nullptr,
-                              e->logits, H, V, 0));
-  } else {
-    TRY(wst_rmsnorm(e->x, m.final_norm, e->h, H, eps));
-    TRY(wst_gemv_int4_hier_ex(head.qw, head.si, head.sb, e->h, nullptr, e->logits, H, V, 0));
-  }
+  TRY(head_logits(e, e->x, fused));
   TRY(mk.mark(WSE_STAGE_HEAD));
   if (e->rs_k > 0) {
     if (fused) {
@@ -552,10 +594,8 @@ static wst_status_t stage_launch(wse_engine *e, int stage, int l, uint64_t *byte
       return wst_gemv_int4_hier_ex(L.down.qw, L.down.si, L.down.sb, e->act, nullptr, e->x, I, H,
                                    1);
     case WSE_STAGE_HEAD: {
-      const Mat &head = m.head();
-      *bytes = head.bytes() + (uint64_t)H * 8 + (uint64_t)V * 4;
-      return wst_gemv_hier_rmsnorm(head.qw, head.si, head.sb, e->x, m.final_norm, eps, e->h,
-                                   nullptr, e->logits, H, V, 0);
+      *bytes = m.head().bytes() + (uint64_t)H * 8 + (uint64_t)V * 4;
+      return head_logits(e, e->x, true);
     }
     default:
       snprintf(g_msg, sizeof(g_msg), "stage %d cannot be timed on its own", stage);
@@ -650,7 +690,11 @@ static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool
   }
   const int pos0 = e->pos;
   TRY(wst_memcpy_h2d(e->c_tokens, ids, (size_t)n * 4));
-  TRY(wst_embed_int4_hier_chunk(m.embed.qw, m.embed.si, m.embed.sb, e->c_tokens, e->c_x, H, V, n));
+  if (m.embed.dense())
+    TRY(wst_embed_fp16_chunk(m.embed.w16, e->c_tokens, e->c_x, H, V, n));
+  else
+    TRY(wst_embed_int4_hier_chunk(m.embed.qw, m.embed.si, m.embed.sb, e->c_tokens, e->c_x, H, V,
+                                  n));
   for (int l = 0; l < c.n_layers; ++l) {
     const Layer &L = m.layers[(size_t)l];
     TRY(wst_rmsnorm_chunk(e->c_x, L.in_norm, e->c_h, H, n, eps));
@@ -667,10 +711,8 @@ static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool
     TRY(wst_gemm_int4_hier(L.down.qw, L.down.si, L.down.sb, e->c_act, nullptr, e->c_x, I, H, n, 1));
   }
   if (want_logits) {
-    const Mat &head = m.head();
     void *last = (char *)e->c_x + (size_t)(n - 1) * H * 4;
-    TRY(wst_rmsnorm(last, m.final_norm, e->h, H, eps));
-    TRY(wst_gemv_int4_hier_ex(head.qw, head.si, head.sb, e->h, nullptr, e->logits, H, V, 0));
+    TRY(head_logits(e, last, false));
     TRY(wst_argmax(e->logits, e->token, V));
   }
   return wse_engine_set_pos(e, pos0 + n);

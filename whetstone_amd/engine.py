@@ -24,7 +24,9 @@ class Config(C.Structure):
         ("n_kv", C.c_int32), ("head_dim", C.c_int32), ("inter", C.c_int32),
         ("vocab", C.c_int32), ("tied", C.c_int32), ("qkv_bias", C.c_int32),
         ("qk_norm", C.c_int32), ("rescore_k", C.c_int32), ("eps", C.c_float),
-        ("rope_theta", C.c_double),
+        ("rope_theta", C.c_double), ("rope_llama3", C.c_int32), ("rope_orig_max", C.c_int32),
+        ("rope_factor", C.c_double), ("rope_low_freq", C.c_double),
+        ("rope_high_freq", C.c_double),
     ]
 
 
@@ -46,6 +48,13 @@ _SIG = {
     "wse_model_tensor": (I32, [P, C.c_char_p, PP, PP, PP, C.POINTER(C.c_int64),
                                C.POINTER(C.c_int64)]),
     "wse_model_weight_bytes": (C.c_uint64, [P]),
+    "wse_model_config": (I32, [P, C.POINTER(Config)]),
+    "wse_model_vector": (I32, [P, C.c_char_p, PP, C.POINTER(C.c_int64)]),
+    "wse_fnv1a": (C.c_uint64, [P, C.c_size_t]),
+    "wse_wstone_check": (I32, [C.c_char_p, I32, C.POINTER(I32)]),
+    "wse_wstone_config": (I32, [C.c_char_p, C.POINTER(Config)]),
+    "wse_config_from_json": (I32, [C.c_char_p, C.POINTER(Config)]),
+    "wse_model_load_wstone": (I32, [C.c_char_p, I32, PP]),
     "wse_engine_create": (I32, [P, I32, I32, PP]),
     "wse_engine_free": (None, [P]),
     "wse_engine_reset": (I32, [P]),
@@ -89,15 +98,65 @@ def _check(st: int) -> None:
         raise ffi.WstError(st, f"{msg} | {kmsg}")
 
 
-class Model:
-    """Seeded synthetic weights, generated and packed in HBM."""
+def _config_dict(c: Config) -> dict:
+    return {name: getattr(c, name) for name, _ in Config._fields_}
 
-    def __init__(self, cfg: dict, seed: int = 0):
+
+def config_from_json(text: str) -> dict:
+    """A config.json parsed and validated as the loader does (config.rs)."""
+    c = Config()
+    _check(lib().wse_config_from_json(text.encode(), C.byref(c)))
+    return _config_dict(c)
+
+
+def wstone_check(path, verify: bool = False) -> int:
+    """Validates a .wstone file's header (and, with verify, every payload
+    hash); returns the tensor count. Raises WstError with the reason."""
+    n = C.c_int32()
+    _check(lib().wse_wstone_check(str(path).encode(), int(verify), C.byref(n)))
+    return n.value
+
+
+def wstone_config(path) -> dict:
+    c = Config()
+    _check(lib().wse_wstone_config(str(path).encode(), C.byref(c)))
+    return _config_dict(c)
+
+
+class Model:
+    """Device-resident weights: seeded synthetic ones generated and packed in
+    HBM, or a .wstone file loaded with Model.load."""
+
+    def __init__(self, cfg: dict | None, seed: int = 0, _handle=None):
+        if _handle is not None:
+            self.h = _handle
+            c = Config()
+            _check(lib().wse_model_config(self.h, C.byref(c)))
+            self.cfg = _config_dict(c)
+            self._c = c
+            return
         self.cfg = dict(cfg)
         self._c = Config(**self.cfg)
         h = C.c_void_p()
         _check(lib().wse_model_synthetic(C.byref(self._c), seed, C.byref(h)))
         self.h = h
+
+    @classmethod
+    def load(cls, path, rescore_k: int = -1) -> "Model":
+        """Loads a .wstone file (model.rs:454-638); rescore_k < 0 enables the
+        top-64 rescore when the file carries the head's f16 copy."""
+        h = C.c_void_p()
+        _check(lib().wse_model_load_wstone(str(path).encode(), rescore_k, C.byref(h)))
+        return cls(None, _handle=h)
+
+    def vector_host(self, name: str) -> np.ndarray:
+        """An f16 tensor of the model (norm gains, biases, the head copy) as
+        f16 bit patterns on the host."""
+        p, n = C.c_void_p(), C.c_int64()
+        _check(lib().wse_model_vector(self.h, name.encode(), C.byref(p), C.byref(n)))
+        out = np.empty(n.value, np.uint16)
+        ffi.check(ffi.lib().wst_memcpy_d2h(out.ctypes.data, p.value, out.nbytes))
+        return out
 
     def tensor(self, name: str):
         qw, si, sb = C.c_void_p(), C.c_void_p(), C.c_void_p()
