@@ -491,3 +491,31 @@ def test_gemm_fp16_matches_matmul(orc, wk, in_f, out_f, n):
     got = y.numpy().reshape(n, out_f).astype(np.float64)
     bound = 1e-5 * (np.abs(xf) @ np.abs(wf).T) + 1e-6
     assert np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,pos0,n,max_seq", [
+    (14, 2, 64, 0, 256, 256), (14, 2, 64, 1000, 44, 1100), (28, 4, 128, 0, 256, 300),
+    (28, 4, 128, 3840, 256, 4096), (8, 8, 128, 5, 1, 16), (7, 1, 64, 2000, 37, 2100)])
+def test_chunk_attention_equals_per_token_decode_attention(orc, wk, n_q, n_kv, hd, pos0, n,
+                                                           max_seq):
+    """Chunk attention (chunk_ops.cu:187-265) is decode attention per token:
+    token j attends to cache positions [0, pos0 + j] (chunk_kernels.rs:262-360)."""
+    rng = np.random.default_rng(pos0 + n + hd)
+    kc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
+    vc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
+    row = (n_q + 2 * n_kv) * hd
+    qkv = (rng.standard_normal(n * row) * 2).astype(np.float32)
+    cache = wk.KvCache(n_kv, n_q, hd, max_seq)
+    cache.k.copy_from(kc.view(np.float16))
+    cache.v.copy_from(vc.view(np.float16))
+    qd = wk.DeviceBuffer.from_array(qkv)
+    out = wk.DeviceBuffer(n * n_q * hd, np.float16)
+    scale = np.float32(1.0 / math.sqrt(hd))
+    ffi.call("wst_attn_chunk", qd.ptr, cache.k.ptr, cache.v.ptr, out.ptr, n_q, n_kv, hd, pos0, n,
+             max_seq, scale)
+    got = out.numpy().astype(np.float64).reshape(n, n_q * hd)
+    for j in range(n):
+        want = np.empty(n_q * hd, np.uint16)
+        q = np.ascontiguousarray(qkv[j * row:j * row + n_q * hd])
+        orc.lib().orc_attn_decode(q, kc, vc, want, n_q, n_kv, hd, pos0 + j, max_seq, scale)
+        assert np.max(np.abs(got[j] - orc.f16_value(want))) < 2e-3, j
