@@ -24,7 +24,8 @@ extern "C" wst_status_t wst_gemm_int4_hier(const void *qw, const void *si, const
   WST_REQUIRE(in_f % 32 == 0, "wst_gemm_int4_hier: in_features must be a multiple of 32");
   WST_REQUIRE(!(((uintptr_t)qw | (uintptr_t)x) & 15u),
               "wst_gemm_int4_hier: qw and x must be 16-byte aligned");
-  wst_gemm_mfma(true, qw, si, sb, x, bias, y, in_f, out_f, n, accum);
+  const wst_status_t st = wst_gemm_mfma(true, qw, si, sb, x, bias, y, in_f, out_f, n, accum);
+  if (st != WST_OK) return st;
   WST_TRY_KERNEL("wst_gemm_int4_hier");
   return WST_OK;
 }
@@ -35,7 +36,9 @@ extern "C" wst_status_t wst_gemm_fp16(const void *w, const void *x, const void *
   WST_REQUIRE(in_f > 0 && out_f > 0 && n > 0, "wst_gemm_fp16: non-positive dimension");
   WST_REQUIRE(in_f % 8 == 0, "wst_gemm_fp16: in_features must be a multiple of 8");
   if (in_f % 32 == 0 && !(((uintptr_t)w | (uintptr_t)x) & 15u)) {
-    wst_gemm_mfma(false, w, nullptr, nullptr, x, bias, y, in_f, out_f, n, accum);
+    const wst_status_t st = wst_gemm_mfma(false, w, nullptr, nullptr, x, bias, y, in_f, out_f, n,
+                                          accum);
+    if (st != WST_OK) return st;
     WST_TRY_KERNEL("wst_gemm_fp16");
     return WST_OK;
   }
@@ -150,24 +153,6 @@ struct AcShape {
   static_assert(16 * (HD + 2) * 4 <= WAVE_HALVES * 2, "the merge rows fit a wave's region");
 };
 
-template <int CTRL>
-__device__ __forceinline__ float ac_dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               CTRL, 0xF, 0xF, false));
-}
-// Over the 16 lanes of a DPP row: quad_perm [1,0,3,2], [2,3,0,1], row_ror:4, :8.
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, ac_dpp<0xB1>(v));
-  v = fmaxf(v, ac_dpp<0x4E>(v));
-  v = fmaxf(v, ac_dpp<0x124>(v));
-  return fmaxf(v, ac_dpp<0x128>(v));
-}
-__device__ __forceinline__ float row16_sum(float v) {
-  v += ac_dpp<0xB1>(v);
-  v += ac_dpp<0x4E>(v);
-  v += ac_dpp<0x124>(v);
-  return v + ac_dpp<0x128>(v);
-}
 // Eight halves as an MFMA operand from two transposing reads (rows r and r + 4
 // of the 16-lane pattern each lane's address selects).
 __device__ __forceinline__ ac_h8 tr_pair(const uint16_t *a0, const uint16_t *a1) {
@@ -281,7 +266,7 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
         const int p = p0 + 16 * t2 + r16;
         sv[t2] = (p <= lim && p < kend) ? sc[t2][i] : -INFINITY;
       }
-      const float mx = row16_max(fmaxf(sv[0], sv[1]));
+      const float mx = dpp_max16(fmaxf(sv[0], sv[1]));
       const float mn = fmaxf(m[i], mx);
       corr[i] = (m[i] == -INFINITY) ? 0.0f : __expf(m[i] - mn);
       float pv[2];
@@ -331,7 +316,7 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   float *mb = (float *)vs;  // this wave's region, [16][HD + 2]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float lr = row16_sum(l[i]);
+    const float lr = dpp_sum16(l[i]);
     const int row = 4 * kg + i;
     if (r16 == 0) {
       mb[row * (HD + 2)] = m[i];

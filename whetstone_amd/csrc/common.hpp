@@ -75,6 +75,7 @@ enum {
   WST_SCRATCH_RESCORE = 2,
   WST_SCRATCH_NLL = 3,
   WST_SCRATCH_ENGINE = 4,
+  WST_SCRATCH_GEMM = 5,  // split-K partial sums of the chunk GEMMs
   WST_SCRATCH_SLOTS = 8
 };
 
