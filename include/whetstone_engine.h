@@ -127,9 +127,27 @@ wst_status_t wse_engine_forward(wse_engine_t *e, int32_t token);
 wst_status_t wse_engine_step(wse_engine_t *e);
 /* Engine::capture_graph (engine.rs:357-393): warm-up step, rewind, capture. */
 wst_status_t wse_engine_capture_graph(wse_engine_t *e);
-/* Chunked prefill of n tokens (engine.rs:748-844), chunks of at most
- * wst_chunk_max_tokens(); the last chunk computes the head for its last row
- * and leaves the greedy pick in the token cursor. */
+/* Engine::chunk_width (engine.rs:682-698): tokens per chunk pass, the
+ * kernels' wst_chunk_max_tokens() or WHETSTONE_CHUNK_WIDTH=k (k >= 1) clamped
+ * to it. */
+wst_status_t wse_engine_chunk_width(wse_engine_t *e, int32_t *out);
+wst_status_t wse_engine_max_seq(const wse_engine_t *e, int32_t *out);
+/* Engine::forward_chunk_ex (engine.rs:731-844): 1 <= n <= chunk width tokens
+ * appended at the current position in one pass over the weights. With
+ * want_logits the final norm, the head (a chunk GEMM over all n rows, no
+ * rescore) and the per-row argmax run; the last row's logits and pick go to
+ * the single-token buffers, so step() and token() continue from there. */
+wst_status_t wse_engine_forward_chunk(wse_engine_t *e, const int32_t *ids_host, int32_t n,
+                                      int32_t want_logits);
+/* Engine::chunk_picks (engine.rs:850-865): the greedy pick of each of the
+ * first n rows of the last chunk pass that computed logits. */
+wst_status_t wse_engine_chunk_picks(wse_engine_t *e, int32_t n, int32_t *out_host);
+/* Engine::rewind (engine.rs:870-881): moves the cache cursor back to pos
+ * (<= the current position); later entries are overwritten, not cleared. */
+wst_status_t wse_engine_rewind(wse_engine_t *e, int32_t pos);
+/* Engine::prefill (engine.rs:890-905): chunks of the chunk width; only the
+ * last chunk computes logits (every row's, as forward_chunk), leaving the
+ * last row's greedy pick in the token cursor. */
 wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids_host, int32_t n,
                                  int32_t chunked);
 /* Greedy generation (engine.rs:909-956): prefill, then n_new tokens, each read
@@ -137,6 +155,28 @@ wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids_host, int32_
 wst_status_t wse_engine_generate(wse_engine_t *e, const int32_t *prompt_host, int32_t n_prompt,
                                  int32_t n_new, int32_t chunked, int32_t *out_tokens_host);
 wst_status_t wse_engine_token(wse_engine_t *e, int32_t *out);
+/* SpecConfig / SpecStats (speculate.rs:58-115). */
+typedef struct {
+  int32_t draft;     /* tokens per verification pass, the confirmed one included */
+  int32_t ngram_max; /* longest n-gram matched against the history */
+  int32_t ngram_min; /* shortest n-gram accepted as a match */
+} wse_spec_config_t;
+typedef struct {
+  int64_t rounds, empty_rounds, proposed, accepted;
+} wse_spec_stats_t;
+/* speculate::propose (speculate.rs:122-150): up to `want` tokens that followed
+ * the most recent earlier occurrence of the history's last n tokens, trying n
+ * from min(ngram_max, n_history - 1) down to ngram_min. Returns the count
+ * written to out (0: no match). Host-only. */
+int32_t wse_spec_propose(const int32_t *history, int32_t n_history, int32_t ngram_max,
+                         int32_t ngram_min, int32_t want, int32_t *out);
+/* speculate::generate (speculate.rs:152-260): greedy generation with the
+ * n-gram draft verified by chunk passes of min(chunk width, draft) tokens.
+ * Writes up to max_new tokens to out_tokens_host and their count to n_out. */
+wst_status_t wse_speculate_generate(wse_engine_t *e, const int32_t *prompt_host, int32_t n_prompt,
+                                    int32_t max_new, const wse_spec_config_t *cfg,
+                                    int32_t *out_tokens_host, int32_t *n_out,
+                                    wse_spec_stats_t *stats);
 /* Writes `token` into the device token cursor (the next step's input). */
 wst_status_t wse_engine_set_token(wse_engine_t *e, int32_t token);
 wst_status_t wse_engine_logits(wse_engine_t *e, float *out_host);

@@ -1,0 +1,120 @@
+"""Chunk passes with per-row picks, rewind, and speculative generation
+(engine.rs:731-881, speculate.rs:152-260) on the GPU.
+
+The reference's exactness claim for speculation: the emitted stream is the
+greedy stream, token for token, because a drafted token is kept only when it
+equals the target's own pick at that position. These tests check it against
+the engine's plain greedy generation. The claim needs the chunk pass's picks
+to equal the decode step's argmax; with a rescored head the decode argmax
+follows the f16 rescore and the chunk head does not (as in the reference), so
+the equality tests use rescore_k = 0.
+"""
+import numpy as np
+import pytest
+
+from whetstone_amd import engine as E
+from whetstone_amd import ffi
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(n_layers=2, hidden=256, n_q=4, n_kv=2, head_dim=64, inter=512, vocab=4096,
+            tied=1, qkv_bias=1, qk_norm=0, rescore_k=0, eps=1e-6, rope_theta=1e6)
+TINY_QK = dict(TINY, n_layers=3, hidden=512, n_q=8, n_kv=2, head_dim=128, inter=1024,
+               vocab=8192, tied=0, qk_norm=1)
+
+
+@pytest.fixture(scope="module", params=[TINY, TINY_QK], ids=["qwen2-tiny", "qknorm-tiny"])
+def model(request):
+    return E.Model(request.param, seed=1)
+
+
+def _prompt(seed, n, vocab):
+    return np.random.default_rng(seed).integers(0, vocab, n).astype(np.int32)
+
+
+def test_chunk_picks_match_per_token_decode(model):
+    V = model.cfg["vocab"]
+    p, x = _prompt(1, 20, V), _prompt(2, 7, V)
+    a, b = E.Engine(model, 128), E.Engine(model, 128)
+    a.prefill(p)
+    b.prefill(p)
+    a.forward_chunk(x)
+    want = []
+    for t in x:
+        b.forward(int(t))
+        want.append(b.token())
+    picks = a.chunk_picks(len(x))
+    assert list(picks) == want
+    assert a.token() == picks[-1] and a.pos == b.pos == 27
+    assert np.allclose(a.logits(), b.logits(), rtol=1e-3, atol=1e-2)
+    assert list(a.chunk_picks(3)) == want[:3]
+
+
+def test_rewind_then_chunk_equals_the_unrejected_history(model):
+    V = model.cfg["vocab"]
+    p, x1, x2 = _prompt(3, 16, V), _prompt(4, 5, V), _prompt(5, 3, V)
+    a, b = E.Engine(model, 128), E.Engine(model, 128)
+    a.prefill(p)
+    b.prefill(p)
+    a.forward_chunk(x1)
+    a.rewind(16 + 2)        # keep x1[:2]; x1[2:] is overwritten by x2
+    a.forward_chunk(x2)
+    b.forward_chunk(x1[:2])
+    b.forward_chunk(x2)
+    assert a.pos == b.pos == 21
+    assert np.array_equal(a.logits().view(np.uint32), b.logits().view(np.uint32))
+    assert np.array_equal(a.chunk_picks(3), b.chunk_picks(3))
+    a.step()                # a decode step continues from the chunk's state
+    b.step()
+    assert np.array_equal(a.logits().view(np.uint32), b.logits().view(np.uint32))
+
+
+def test_chunk_errors(model):
+    e = E.Engine(model, 64)
+    with pytest.raises(ffi.WstError, match="no chunk pass"):
+        e.chunk_picks(1)
+    with pytest.raises(ffi.WstError, match="empty chunk"):
+        e.forward_chunk(np.zeros(0, np.int32))
+    w = e.chunk_width()
+    with pytest.raises(ffi.WstError, match="chunk width"):
+        e.forward_chunk(np.zeros(w + 1, np.int32))
+    e.forward_chunk(np.array([1, 2, 3], np.int32))
+    with pytest.raises(ffi.WstError, match="chunk width"):
+        e.chunk_picks(w + 1)
+    with pytest.raises(ffi.WstError, match="ahead of the current position"):
+        e.rewind(4)
+    with pytest.raises(ffi.WstError, match="exceeds the 64 token cache"):
+        e.forward_chunk(np.zeros(62, np.int32))
+    e.rewind(0)
+    assert e.pos == 0
+
+
+@pytest.mark.parametrize("graph", [False, True], ids=["eager", "graph"])
+def test_speculation_emits_the_greedy_stream(model, graph):
+    V = model.cfg["vocab"]
+    base = _prompt(6, 5, V)
+    prompt = np.concatenate([base] * 4 + [base[:3]])  # repeats for the draft
+    n_new = 64
+    ref = E.Engine(model, 256)
+    want = ref.generate(prompt, n_new)
+    e = E.Engine(model, 256)
+    if graph:
+        e.capture_graph()
+        e.reset()
+    got, st = e.speculate(prompt, n_new, E.SpecConfig(draft=4))
+    assert list(got) == list(want)
+    assert st.rounds > 0 and st.proposed > 0
+    assert st.rounds - st.empty_rounds <= st.rounds
+    # every round emits its confirmed token plus the accepted drafts
+    assert st.rounds + st.accepted >= n_new - 1
+    print(f"acceptance {st.acceptance():.2f}, tokens/round {st.tokens_per_round():.2f}")
+
+
+def test_speculation_at_the_end_of_the_cache(model):
+    V = model.cfg["vocab"]
+    prompt = np.concatenate([_prompt(7, 4, V)] * 3)
+    ref = E.Engine(model, 20)
+    want = ref.generate(prompt, 20)  # the cache fills after 20 - 12 + 1 tokens
+    e = E.Engine(model, 20)
+    got, _ = e.speculate(prompt, 20, E.SpecConfig(draft=8))
+    assert len(got) == 9 and list(got) == list(want[:9]) and e.pos == 20

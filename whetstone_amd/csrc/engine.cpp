@@ -6,8 +6,10 @@
 // crosses -- and is compiled as plain host C++.
 #include "whetstone_engine.h"
 
+#include <errno.h>
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -54,6 +56,8 @@ struct wse_engine {
   int chunk_width = 0;
   void *c_tokens = nullptr, *c_x = nullptr, *c_h = nullptr, *c_qkv = nullptr, *c_attn = nullptr,
        *c_gu = nullptr, *c_act = nullptr;
+  void *c_logits = nullptr, *c_picks = nullptr;  // the chunk head's, on first use
+  bool c_ran = false;                            // a chunk pass has left picks
   std::vector<void *> events;
   Arena arena;
 };
@@ -657,10 +661,28 @@ uint64_t wse_engine_step_bytes(const wse_engine_t *e) {
 
 // ---------------------------------------------------------------- prefill
 
+// Engine::chunk_width (engine.rs:682-698): the chunk kernels' width, or
+// WHETSTONE_CHUNK_WIDTH=k (an integer >= 1) clamped to it.
+static int configured_chunk_width() {
+  static int w = 0;
+  if (w == 0) {
+    const int mx = wst_chunk_max_tokens();
+    w = mx;
+    if (const char *s = getenv("WHETSTONE_CHUNK_WIDTH")) {
+      char *end = nullptr;
+      errno = 0;
+      const unsigned long long k = strtoull(s, &end, 10);
+      if (*s >= '0' && *s <= '9' && end && *end == '\0' && errno == 0 && k >= 1)
+        w = k < (unsigned long long)mx ? (int)k : mx;
+    }
+  }
+  return w;
+}
+
 static wst_status_t ensure_chunk(wse_engine *e) {
   if (e->chunk_width) return WST_OK;
   const wse_config_t &c = e->m->c;
-  const size_t w = (size_t)wst_chunk_max_tokens();
+  const size_t w = (size_t)configured_chunk_width();
   const size_t H = (size_t)c.hidden, hd = (size_t)c.head_dim, I = (size_t)c.inter;
   const size_t nqkv = (size_t)(c.n_q + 2 * c.n_kv) * hd;
   Arena &a = e->arena;
@@ -675,8 +697,19 @@ static wst_status_t ensure_chunk(wse_engine *e) {
   return WST_OK;
 }
 
-// Engine::forward_chunk_ex (engine.rs:748-844). The head runs only for the
-// chunk's last row, on the single-token buffers, when want_logits.
+// The chunk head's outputs: n x vocab f32 logits and n picks.
+static wst_status_t ensure_chunk_head(wse_engine *e) {
+  if (e->c_logits) return WST_OK;
+  const size_t w = (size_t)e->chunk_width, V = (size_t)e->m->c.vocab;
+  TRY(e->arena.alloc(&e->c_logits, w * V * 4, false));
+  TRY(e->arena.alloc(&e->c_picks, w * 4, true));
+  return WST_OK;
+}
+
+// Engine::forward_chunk_ex (engine.rs:748-844). With want_logits the final
+// norm and the head (a plain chunk GEMM: no rescore) run for every row, the
+// chunk argmax leaves each row's greedy pick, and the last row's logits and
+// pick are copied to the single-token buffers (logits, token cursor).
 static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool want_logits) {
   const wse_model &m = *e->m;
   const wse_config_t &c = m.c;
@@ -684,7 +717,7 @@ static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool
   const int nqkv = (nq + 2 * nkv) * hd;
   const float eps = c.eps, scale = (float)(1.0 / sqrt((double)hd));
   if (e->pos + n > e->max_seq) {
-    snprintf(g_msg, sizeof(g_msg), "prefill: %d tokens at position %d exceed the %d token cache",
+    snprintf(g_msg, sizeof(g_msg), "forward_chunk: %d tokens at position %d exceeds the %d token cache",
              n, e->pos, e->max_seq);
     return WST_ERR_SHAPE;
   }
@@ -711,11 +744,74 @@ static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool
     TRY(wst_gemm_int4_hier(L.down.qw, L.down.si, L.down.sb, e->c_act, nullptr, e->c_x, I, H, n, 1));
   }
   if (want_logits) {
-    void *last = (char *)e->c_x + (size_t)(n - 1) * H * 4;
-    TRY(head_logits(e, last, false));
-    TRY(wst_argmax(e->logits, e->token, V));
+    const Mat &head = m.head();
+    TRY(ensure_chunk_head(e));
+    TRY(wst_rmsnorm_chunk(e->c_x, m.final_norm, e->c_h, H, n, eps));
+    if (head.dense())
+      TRY(wst_gemm_fp16(head.w16, e->c_h, nullptr, e->c_logits, H, V, n, 0));
+    else
+      TRY(wst_gemm_int4_hier(head.qw, head.si, head.sb, e->c_h, nullptr, e->c_logits, H, V, n, 0));
+    TRY(wst_argmax_chunk(e->c_logits, e->c_picks, V, n));
+    TRY(wst_memcpy_d2d(e->logits, (const char *)e->c_logits + (size_t)(n - 1) * V * 4,
+                       (size_t)V * 4));
+    TRY(wst_memcpy_d2d(e->token, (const char *)e->c_picks + (size_t)(n - 1) * 4, 4));
+    e->c_ran = true;
   }
   return wse_engine_set_pos(e, pos0 + n);
+}
+
+wst_status_t wse_engine_max_seq(const wse_engine_t *e, int32_t *out) {
+  if (!e || !out) return WST_ERR_INVALID_ARG;
+  *out = e->max_seq;
+  return WST_OK;
+}
+
+wst_status_t wse_engine_chunk_width(wse_engine_t *e, int32_t *out) {
+  if (!e || !out) return WST_ERR_INVALID_ARG;
+  *out = configured_chunk_width();
+  return WST_OK;
+}
+
+wst_status_t wse_engine_forward_chunk(wse_engine_t *e, const int32_t *ids, int32_t n,
+                                      int32_t want_logits) {
+  if (!e || !ids) return WST_ERR_INVALID_ARG;
+  if (n <= 0) {
+    snprintf(g_msg, sizeof(g_msg), "forward_chunk: empty chunk");
+    return WST_ERR_SHAPE;
+  }
+  TRY(ensure_chunk(e));
+  if (n > e->chunk_width) {
+    snprintf(g_msg, sizeof(g_msg), "forward_chunk: %d tokens exceeds the %d token chunk width", n,
+             e->chunk_width);
+    return WST_ERR_SHAPE;
+  }
+  return forward_chunk(e, ids, n, want_logits != 0);
+}
+
+wst_status_t wse_engine_chunk_picks(wse_engine_t *e, int32_t n, int32_t *out) {
+  if (!e || !out || n < 0) return WST_ERR_INVALID_ARG;
+  if (!e->c_ran) {
+    snprintf(g_msg, sizeof(g_msg), "no chunk pass has run");
+    return WST_ERR_SHAPE;
+  }
+  if (n > e->chunk_width) {
+    snprintf(g_msg, sizeof(g_msg), "chunk_picks: %d exceeds the %d token chunk width", n,
+             e->chunk_width);
+    return WST_ERR_SHAPE;
+  }
+  if (n == 0) return WST_OK;
+  TRY(wst_memcpy_d2h(out, e->c_picks, (size_t)n * 4));
+  for (int i = 0; i < n; ++i) out[i] = out[i] < 0 ? 0 : out[i];  // v.max(0)
+  return WST_OK;
+}
+
+wst_status_t wse_engine_rewind(wse_engine_t *e, int32_t pos) {
+  if (!e || pos < 0) return WST_ERR_INVALID_ARG;
+  if (pos > e->pos) {
+    snprintf(g_msg, sizeof(g_msg), "rewind: %d is ahead of the current position %d", pos, e->pos);
+    return WST_ERR_SHAPE;
+  }
+  return wse_engine_set_pos(e, pos);
 }
 
 wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids, int32_t n, int32_t chunked) {

@@ -72,7 +72,42 @@ _SIG = {
     "wse_engine_profile_step": (I32, [P, C.POINTER(C.c_double), C.POINTER(I32)]),
     "wse_engine_step_bytes": (C.c_uint64, [P]),
     "wse_engine_time_stage": (I32, [P, I32, I32, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
+    "wse_engine_max_seq": (I32, [P, C.POINTER(I32)]),
+    "wse_engine_chunk_width": (I32, [P, C.POINTER(I32)]),
+    "wse_engine_forward_chunk": (I32, [P, P, I32, I32]),
+    "wse_engine_chunk_picks": (I32, [P, I32, P]),
+    "wse_engine_rewind": (I32, [P, I32]),
+    "wse_spec_propose": (I32, [P, I32, I32, I32, I32, P]),
+    "wse_speculate_generate": (I32, [P, P, I32, I32, P, P, C.POINTER(I32), P]),
 }
+
+
+class SpecConfig(C.Structure):
+    """wse_spec_config_t (speculate.rs SpecConfig); defaults of its Default."""
+    _fields_ = [("draft", C.c_int32), ("ngram_max", C.c_int32), ("ngram_min", C.c_int32)]
+
+    def __init__(self, draft: int = 4, ngram_max: int = 3, ngram_min: int = 2):
+        super().__init__(draft, ngram_max, ngram_min)
+
+
+class SpecStats(C.Structure):
+    """wse_spec_stats_t (speculate.rs SpecStats)."""
+    _fields_ = [("rounds", C.c_int64), ("empty_rounds", C.c_int64), ("proposed", C.c_int64),
+                ("accepted", C.c_int64)]
+
+    def acceptance(self) -> float:
+        return self.accepted / self.proposed if self.proposed else 0.0
+
+    def tokens_per_round(self) -> float:
+        return (self.rounds + self.accepted) / self.rounds if self.rounds else 0.0
+
+
+def spec_propose(history, ngram_max: int = 3, ngram_min: int = 2, want: int = 3) -> list[int]:
+    """speculate.rs propose: the n-gram draft (host code in the engine library)."""
+    h = np.ascontiguousarray(history, np.int32)
+    out = np.zeros(max(want, 1), np.int32)
+    n = lib().wse_spec_propose(h.ctypes.data, h.size, ngram_max, ngram_min, want, out.ctypes.data)
+    return [int(v) for v in out[:n]]
 _lib = None
 
 
@@ -234,6 +269,33 @@ class Engine:
         _check(lib().wse_engine_generate(self.h, a.ctypes.data, a.size, n_new, int(chunked),
                                          out.ctypes.data))
         return out[:n_new]
+
+    def chunk_width(self) -> int:
+        w = C.c_int32()
+        _check(lib().wse_engine_chunk_width(self.h, C.byref(w)))
+        return w.value
+
+    def forward_chunk(self, ids, want_logits: bool = True):
+        a = np.ascontiguousarray(ids, np.int32)
+        _check(lib().wse_engine_forward_chunk(self.h, a.ctypes.data, a.size, int(want_logits)))
+
+    def chunk_picks(self, n: int) -> np.ndarray:
+        out = np.zeros(max(n, 1), np.int32)
+        _check(lib().wse_engine_chunk_picks(self.h, n, out.ctypes.data))
+        return out[:n]
+
+    def rewind(self, pos: int):
+        _check(lib().wse_engine_rewind(self.h, pos))
+
+    def speculate(self, prompt, max_new: int, cfg: SpecConfig | None = None):
+        """speculate::generate: (tokens, SpecStats)."""
+        a = np.ascontiguousarray(prompt, np.int32)
+        cfg = SpecConfig() if cfg is None else cfg
+        out = np.zeros(max(max_new, 1), np.int32)
+        n, st = C.c_int32(), SpecStats()
+        _check(lib().wse_speculate_generate(self.h, a.ctypes.data, a.size, max_new, C.byref(cfg),
+                                            out.ctypes.data, C.byref(n), C.byref(st)))
+        return out[:n.value], st
 
     def set_token(self, token: int):
         _check(lib().wse_engine_set_token(self.h, token))
