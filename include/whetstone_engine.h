@@ -193,6 +193,15 @@ wst_status_t wse_engine_profile_step(wse_engine_t *e, double *stage_ms, int32_t 
  * the same values; the position and token cursor are unchanged. */
 wst_status_t wse_engine_time_stage(wse_engine_t *e, int32_t stage, int32_t reps,
                                    double *us_per_launch, uint64_t *bytes_per_launch);
+/* Engine::cross_entropy (engine.rs:585-618): for each of the first
+ * min(n_tokens / window, max_windows) windows, reset the cache and feed
+ * tokens 0..window-2 of the window, adding -log softmax(logits)[next token]
+ * on the device (wst_nll). Returns the summed NLL (nats) and the number of
+ * predicted positions; perplexity = exp(nll_sum / positions). The window must
+ * hold at least 2 tokens and fit the cache (WST_ERR_SHAPE otherwise). */
+wst_status_t wse_engine_cross_entropy(wse_engine_t *e, const int32_t *tokens_host,
+                                      int64_t n_tokens, int32_t window, int32_t max_windows,
+                                      double *nll_sum, int64_t *positions);
 /* Algorithmic bytes of one decode step at the current position. */
 uint64_t wse_engine_step_bytes(const wse_engine_t *e);
 

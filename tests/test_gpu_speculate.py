@@ -118,3 +118,46 @@ def test_speculation_at_the_end_of_the_cache(model):
     e = E.Engine(model, 20)
     got, _ = e.speculate(prompt, 20, E.SpecConfig(draft=8))
     assert len(got) == 9 and list(got) == list(want[:9]) and e.pos == 20
+
+
+# ------------------------------------------------ Engine::cross_entropy
+
+def _host_nll(logits, target):
+    z = np.asarray(logits, np.float64)
+    m = z.max()
+    return float(m + np.log(np.exp(z - m).sum()) - z[target])
+
+
+def test_cross_entropy_matches_per_window_decode_and_host_log_softmax(model):
+    """engine.rs:585-618: each window from an empty cache, position i predicts
+    token i+1; the device sum equals the host log-softmax of the same logits."""
+    V, W = model.cfg["vocab"], 9
+    toks = _prompt(5, 3 * W + 4, V)  # 3 whole windows and a ragged tail
+    a, b = E.Engine(model, 64), E.Engine(model, 64)
+    nll, n = a.cross_entropy(toks, W)
+    want = 0.0
+    for w in range(3):
+        b.reset()
+        for i in range(W - 1):
+            b.forward(int(toks[w * W + i]))
+            want += _host_nll(b.logits(), int(toks[w * W + i + 1]))
+    assert n == 3 * (W - 1)
+    assert abs(nll - want) <= 1e-5 * abs(want) + 1e-3, (nll, want)
+    # max_windows bounds the windows; one window is its own (sum, count)
+    nll1, n1 = a.cross_entropy(toks, W, max_windows=1)
+    assert n1 == W - 1 and 0.0 < nll1 < nll
+    # random weights give near-uniform predictions: per-position NLL ~ log V
+    assert abs(nll / n - np.log(V)) < 0.5
+
+
+def test_cross_entropy_refusals(model):
+    e = E.Engine(model, 16)
+    toks = _prompt(6, 40, model.cfg["vocab"])
+    for window in (0, 1, 17):
+        with pytest.raises(ffi.WstError):
+            e.cross_entropy(toks, window)
+    bad = toks.copy()
+    bad[3] = model.cfg["vocab"]
+    with pytest.raises(ffi.WstError):
+        e.cross_entropy(bad, 8)
+    assert e.cross_entropy(toks[:5], 8) == (0.0, 0)  # no whole window

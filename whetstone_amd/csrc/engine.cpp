@@ -57,6 +57,7 @@ struct wse_engine {
   void *c_tokens = nullptr, *c_x = nullptr, *c_h = nullptr, *c_qkv = nullptr, *c_attn = nullptr,
        *c_gu = nullptr, *c_act = nullptr;
   void *c_logits = nullptr, *c_picks = nullptr;  // the chunk head's, on first use
+  void *nll_acc = nullptr;                       // cross_entropy's (sum, count), on first use
   bool c_ran = false;                            // a chunk pass has left picks
   std::vector<void *> events;
   Arena arena;
@@ -649,6 +650,51 @@ wst_status_t wse_engine_set_token(wse_engine_t *e, int32_t token) {
 wst_status_t wse_engine_logits(wse_engine_t *e, float *out) {
   if (!e || !out) return WST_ERR_INVALID_ARG;
   return wst_memcpy_d2h(out, e->logits, (size_t)e->m->c.vocab * 4);
+}
+
+// Engine::cross_entropy (engine.rs:585-618): windows of `window` tokens, each
+// from an empty cache; position i predicts token i+1 (i < window-1), its
+// -log softmax accumulated on the device by wst_nll. Only the two floats come
+// back, once per window.
+wst_status_t wse_engine_cross_entropy(wse_engine_t *e, const int32_t *tokens, int64_t n_tokens,
+                                      int32_t window, int32_t max_windows, double *nll_sum,
+                                      int64_t *positions) {
+  if (!e || !nll_sum || !positions || n_tokens < 0 || max_windows < 0 ||
+      (n_tokens > 0 && !tokens))
+    return WST_ERR_INVALID_ARG;
+  if (window < 2) {
+    snprintf(g_msg, sizeof(g_msg), "window must be at least 2 tokens");
+    return WST_ERR_SHAPE;
+  }
+  if (window > e->max_seq) {
+    snprintf(g_msg, sizeof(g_msg), "window %d exceeds the %d token cache; raise --ctx", window,
+             e->max_seq);
+    return WST_ERR_SHAPE;
+  }
+  const int32_t vocab = e->m->c.vocab;
+  for (int64_t i = 0; i < n_tokens; ++i)
+    if (tokens[i] < 0 || tokens[i] >= vocab) {
+      snprintf(g_msg, sizeof(g_msg), "token %d at %lld is outside the vocabulary", tokens[i],
+               (long long)i);
+      return WST_ERR_INVALID_ARG;
+    }
+  if (!e->nll_acc) TRY(e->arena.alloc(&e->nll_acc, 8, true));
+  TRY(wst_memset(e->nll_acc, 0, 8));
+  int64_t n = n_tokens / window;
+  if (n > max_windows) n = max_windows;
+  for (int64_t w = 0; w < n; ++w) {
+    TRY(wse_engine_reset(e));
+    const int32_t *chunk = tokens + w * window;
+    for (int i = 0; i < window - 1; ++i) {
+      TRY(wse_engine_forward(e, chunk[i]));
+      TRY(wst_nll(e->logits, chunk[i + 1], e->nll_acc, vocab));
+    }
+  }
+  float got[2];
+  TRY(wst_memcpy_d2h(got, e->nll_acc, 8));
+  *nll_sum = (double)got[0];
+  *positions = (int64_t)got[1];
+  return WST_OK;
 }
 
 uint64_t wse_engine_step_bytes(const wse_engine_t *e) {

@@ -77,6 +77,8 @@ _SIG = {
     "wse_engine_forward_chunk": (I32, [P, P, I32, I32]),
     "wse_engine_chunk_picks": (I32, [P, I32, P]),
     "wse_engine_rewind": (I32, [P, I32]),
+    "wse_engine_cross_entropy": (I32, [P, P, C.c_int64, I32, I32, C.POINTER(C.c_double),
+                                       C.POINTER(C.c_int64)]),
     "wse_spec_propose": (I32, [P, I32, I32, I32, I32, P]),
     "wse_speculate_generate": (I32, [P, P, I32, I32, P, P, C.POINTER(I32), P]),
 }
@@ -296,6 +298,14 @@ class Engine:
         _check(lib().wse_speculate_generate(self.h, a.ctypes.data, a.size, max_new, C.byref(cfg),
                                             out.ctypes.data, C.byref(n), C.byref(st)))
         return out[:n.value], st
+
+    def cross_entropy(self, tokens, window: int, max_windows: int = 1 << 30):
+        """Engine::cross_entropy: (summed NLL in nats, predicted positions)."""
+        a = np.ascontiguousarray(tokens, np.int32)
+        nll, n = C.c_double(), C.c_int64()
+        _check(lib().wse_engine_cross_entropy(self.h, a.ctypes.data, a.size, window, max_windows,
+                                              C.byref(nll), C.byref(n)))
+        return nll.value, n.value
 
     def set_token(self, token: int):
         _check(lib().wse_engine_set_token(self.h, token))
