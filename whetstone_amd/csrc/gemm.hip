@@ -40,10 +40,11 @@
 #define GM_KG 4                                   // groups per step
 #define GM_KC (GM_KG * HGROUP)                    // columns per step
 #define GM_KS (GM_KC + 8)                         // LDS row stride (halves): conflict-free reads
-#define GM_XP (GM_BN * GM_KC / 8 / GM_THREADS)    // 16-byte x pieces per thread per step
 #define GM_WT (GM_BM * GM_KS)                     // halves of one W buffer
-#define GM_XT (GM_BN * GM_KS)                     // halves of one x buffer
-#define GM_LDS ((2 * GM_WT + 2 * GM_XT) * 2)      // bytes
+#define GM_LDS (2 * GM_WT * 2)                    // bytes: the W double buffer only
+#define GM_NKK (GM_KC / 32)                       // MFMA k-steps per step
+#define GM_CS (GM_BM + 4)                         // epilogue tile row stride (floats)
+static_assert(GM_BN * GM_CS * 4 <= GM_LDS, "the epilogue tile reuses the W buffers");
 
 typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
 typedef float gm_f4 __attribute__((ext_vector_type(4)));
@@ -52,6 +53,16 @@ typedef uint32_t gm_u4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ gm_h8 gm_lds8(const uint16_t *p) {
   return __builtin_bit_cast(gm_h8, *(const gm_u4 *)p);
 }
+
+// One step's operands in registers: this thread's W piece (packed, or four
+// f16 pieces) and this wave's x B-operand fragments, loaded straight from
+// memory in the MFMA layout (lane l: token l%16, columns 8*(l/16)..+7).
+template <bool HIER>
+struct GmStage {
+  gm_u4 wv[HIER ? 1 : 4];
+  uint32_t widx;
+  gm_u4 xb[GM_NKK][2];
+};
 
 // HIER: w = (qw, si, sb) int4-hier-g32; else w is f16 [out_f][in_f].
 // Split z = blockIdx.z covers groups [z*gps, min(G, (z+1)*gps)); with one
@@ -63,8 +74,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
     float *__restrict__ ws, int in_f, int out_f, int n, int accum, int gps) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint16_t gm_lds[];
-  uint16_t *wt = gm_lds;            // [2][GM_BM][GM_KS]
-  uint16_t *xt = gm_lds + 2 * GM_WT;  // [2][GM_BN][GM_KS]
+  uint16_t *wt = gm_lds;  // [2][GM_BM][GM_KS]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r0 = blockIdx.x * GM_BM, t0 = blockIdx.y * GM_BN;
   const int G = in_f / HGROUP;
@@ -80,56 +90,57 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
     d = h2f((uint16_t)(p & 0xFFFFu));
     dm = h2f((uint16_t)(p >> 16));
   }
-  gm_u4 wv[HIER ? 1 : 4];
-  uint32_t widx = 0;
-  gm_u4 xv[GM_XP];
-  auto load = [&](int step) {  // indices clamped: unconditional loads stay batched
+  const int r16 = lane & 15, kq = (lane >> 4) * 8;
+  const uint16_t *xrow[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+    xrow[b] = x + (size_t)min(t0 + wave * 32 + b * 16 + r16, n - 1) * in_f + kq;
+
+  // Loads are unconditional (the step clamped to the last one): a load under
+  // a branch would be followed by a wait for every load in flight.
+  auto load = [&](GmStage<HIER> &S, int step) {
+    step = min(step, steps - 1);
     const int g = g_begin + step * GM_KG;
     const int gw = min(g + wg, G - 1);
     if constexpr (HIER) {
-      wv[0] = *(const gm_u4 *)((const uint32_t *)w + (size_t)wrow * (in_f / 8) + gw * 4);
-      widx = si[(size_t)wrow * G + gw];
+      S.wv[0] = *(const gm_u4 *)((const uint32_t *)w + (size_t)wrow * (in_f / 8) + gw * 4);
+      S.widx = si[(size_t)wrow * G + gw];
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        wv[i] = *(const gm_u4 *)((const uint16_t *)w + (size_t)wrow * in_f + gw * HGROUP + 8 * i);
+        S.wv[i] = *(const gm_u4 *)((const uint16_t *)w + (size_t)wrow * in_f + gw * HGROUP + 8 * i);
     }
 #pragma unroll
-    for (int i = 0; i < GM_XP; ++i) {
-      const int piece = tid + GM_THREADS * i;
-      const int tok = min(t0 + piece / (GM_KC / 8), n - 1);
-      const int col = min(g * HGROUP + 8 * (piece % (GM_KC / 8)), in_f - 8);
-      xv[i] = *(const gm_u4 *)(x + (size_t)tok * in_f + col);
+    for (int k = 0; k < GM_NKK; ++k) {
+      const int col = min(g * HGROUP + 32 * k, in_f - 32);  // past G: any finite columns
+#pragma unroll
+      for (int b = 0; b < 2; ++b) S.xb[k][b] = *(const gm_u4 *)(xrow[b] + col);
     }
   };
-  auto store = [&](int step, int buf) {
+  auto store = [&](const GmStage<HIER> &S, int step, int buf) {
     // Groups past the split's range hold zero weights (their x is finite).
     const bool live = g_begin + step * GM_KG + wg < g_end;
     uint16_t *dst = wt + buf * GM_WT + wr * GM_KS + wg * HGROUP;
     if constexpr (HIER) {
-      const float s = __fmul_rn(d, (float)(widx & 0xFu));
-      const float m = __fmul_rn(-dm, (float)(widx >> 4));
+      // A dead group gets s = m = 0 (every weight +0) by select, not by a
+      // branch: a branch here makes the compiler wait for every load in flight.
+      const float s = live ? __fmul_rn(d, (float)(S.widx & 0xFu)) : 0.0f;
+      const float m = live ? __fmul_rn(-dm, (float)(S.widx >> 4)) : 0.0f;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const uint32_t word = wv[0][q4];
+        const uint32_t word = S.wv[0][q4];
         uint32_t hv[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const float lo = __fadd_rn(__fmul_rn((float)((word >> (8 * k)) & 0xFu), s), m);
           const float hi = __fadd_rn(__fmul_rn((float)((word >> (8 * k + 4)) & 0xFu), s), m);
-          hv[k] = live ? ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16)) : 0u;
+          hv[k] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
         }
         *(gm_u4 *)(dst + 8 * q4) = (gm_u4){hv[0], hv[1], hv[2], hv[3]};
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *(gm_u4 *)(dst + 8 * i) = live ? wv[i] : (gm_u4){0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < GM_XP; ++i) {
-      const int piece = tid + GM_THREADS * i;
-      *(gm_u4 *)(xt + buf * GM_XT + (piece / (GM_KC / 8)) * GM_KS + 8 * (piece % (GM_KC / 8))) =
-          xv[i];
+      for (int i = 0; i < 4; ++i) *(gm_u4 *)(dst + 8 * i) = S.wv[i] & (gm_u4)(live ? ~0u : 0u);
     }
   };
 
@@ -139,54 +150,95 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[a][b] = (gm_f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-  load(0);
-  store(0, 0);
-  __syncthreads();
-  const int r16 = lane & 15, kq = (lane >> 4) * 8;
-  for (int st = 0; st < steps; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < steps) load(st + 1);
-    const uint16_t *wb = wt + buf * GM_WT, *xb = xt + buf * GM_XT;
+  auto compute = [&](const GmStage<HIER> &S, int buf) {
+    const uint16_t *wb = wt + buf * GM_WT;
 #pragma unroll
-    for (int kk = 0; kk < GM_KC; kk += 32) {
-      gm_h8 bf[2];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) bf[b] = gm_lds8(xb + (wave * 32 + b * 16 + r16) * GM_KS + kk + kq);
+    for (int k = 0; k < GM_NKK; ++k) {
+      const gm_h8 bf0 = __builtin_bit_cast(gm_h8, S.xb[k][0]);
+      const gm_h8 bf1 = __builtin_bit_cast(gm_h8, S.xb[k][1]);
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const gm_h8 af = gm_lds8(wb + (a * 16 + r16) * GM_KS + kk + kq);
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[a][b], 0, 0, 0);
+        const gm_h8 af = gm_lds8(wb + (a * 16 + r16) * GM_KS + 32 * k + kq);
+        acc[a][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf0, acc[a][0], 0, 0, 0);
+        acc[a][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf1, acc[a][1], 0, 0, 0);
       }
     }
-    if (st + 1 < steps) store(st + 1, buf ^ 1);
+  };
+
+  // Three register stages rotate, so two steps' loads are always in flight
+  // behind the one being multiplied; the W tile of step st sits in LDS
+  // buffer st & 1, written from its registers one step ahead. The order of
+  // the products (k ascending) is that of a plain K loop. (Measured against
+  // running whole rounds of three steps, which keeps every wait partial but
+  // multiplies up to two steps of zero weights: slower, 76k against 93k tok/s
+  // of config-4 prefill.)
+  GmStage<HIER> S0, S1, S2;
+  load(S0, 0);
+  load(S1, 1);
+  store(S0, 0, 0);
+  __syncthreads();
+  for (int st = 0; st < steps; st += 3) {
+    load(S2, st + 2);
+    compute(S0, st & 1);
+    store(S1, st + 1, (st + 1) & 1);
+    __syncthreads();
+    if (st + 1 >= steps) break;
+    load(S0, st + 3);
+    compute(S1, (st + 1) & 1);
+    store(S2, st + 2, st & 1);
+    __syncthreads();
+    if (st + 2 >= steps) break;
+    load(S1, st + 4);
+    compute(S2, st & 1);
+    store(S0, st + 3, (st + 1) & 1);
     __syncthreads();
   }
 
-  // C[row][token]: lane holds rows 4*(lane/16)+i of each 16-row tile, token lane%16.
-  const bool split = gridDim.z > 1;
-  float *part = split ? ws + (size_t)blockIdx.z * n * out_f : nullptr;
+  // Epilogue through LDS: C[row][token] (lane: rows 4*(lane/16)+i of each
+  // 16-row tile, token lane%16) is stored token-major into the W buffers
+  // (free after the loop's last barrier), then each token's 64 rows go out as
+  // contiguous 16-byte pieces. Written straight from the accumulators, the
+  // f32 outputs were 4-byte stores scattered over 16 rows per instruction, and
+  // they cost more than the whole K loop (the gate|up tile: 16 of 28 us).
+  float *ct = (float *)gm_lds;  // [GM_BN][GM_CS]
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int tok = t0 + wave * 32 + b * 16 + r16;
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = r0 + a * 16 + (lane >> 4) * 4 + i;
-        if (row < out_f && tok < n) {
-          float v = acc[a][b][i];
-          if (split) {
-            part[(size_t)tok * out_f + row] = v;
-          } else {
-            if (bias) v += h2f(bias[row]);
-            float *dst = y + (size_t)tok * out_f + row;
-            *dst = accum ? *dst + v : v;
-          }
-        }
-      }
+      for (int i = 0; i < 4; ++i)
+        ct[(wave * 32 + b * 16 + r16) * GM_CS + a * 16 + (lane >> 4) * 4 + i] = acc[a][b][i];
+  __syncthreads();
+  const bool split = gridDim.z > 1;
+  float *dst0 = split ? ws + (size_t)blockIdx.z * n * out_f : y;
+  const bool vec = (out_f & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < GM_BM * GM_BN / 4 / GM_THREADS; ++j) {
+    const int idx = tid + GM_THREADS * j;
+    const int tl = idx / (GM_BM / 4), rl = (idx % (GM_BM / 4)) * 4;
+    const int tok = t0 + tl, row = r0 + rl;
+    if (tok >= n || row >= out_f) continue;
+    float v[4];
+    const float4 cv = *(const float4 *)(ct + tl * GM_CS + rl);
+    v[0] = cv.x; v[1] = cv.y; v[2] = cv.z; v[3] = cv.w;
+    float *dst = dst0 + (size_t)tok * out_f + row;
+    if (!split) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (bias && row + e < out_f) v[e] += h2f(bias[row + e]);
     }
+    if (vec) {  // out_f % 4 == 0: the four rows exist and the piece is aligned
+      if (!split && accum) {
+        const float4 o = *(const float4 *)dst;
+        v[0] = o.x + v[0]; v[1] = o.y + v[1]; v[2] = o.z + v[2]; v[3] = o.w + v[3];
+      }
+      *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (row + e < out_f) dst[e] = (!split && accum) ? dst[e] + v[e] : v[e];
+    }
+  }
 }
 
 // y = (accum ? y : 0) + (sum of the splits in split order) + bias.
