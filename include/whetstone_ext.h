@@ -93,6 +93,34 @@ wst_status_t wst_head_rescore_fused(const void *head, const void *x, void *logit
                                     int32_t n, int32_t hidden, int32_t k, int32_t cap,
                                     void *scratch, int32_t nblocks);
 
+/* Chunk (prefill) fused forms, each bit-identical to the unfused ABI sequence
+ * it replaces (tested so):
+ *
+ * wst_gemm_int4_hier(gate|up, x -> gu [n][2*inter]) + wst_swiglu_chunk(gu ->
+ * act): act f16 [n][inter]; qw/si/sb are the fused gate|up matrix
+ * [2*inter][in_f] (gate rows first). */
+wst_status_t wst_gemm_hier_swiglu_chunk(const void *qw, const void *si, const void *sb,
+                                        const void *x, void *act, int32_t in_f, int32_t inter,
+                                        int32_t n);
+/* wst_gemm_int4_hier(..., y, accum) + wst_rmsnorm_chunk(y, norm_w, h_out):
+ * y f32 [n][out_f] (the residual stream), h_out f16 [n][out_f];
+ * out_f <= 16384. */
+wst_status_t wst_gemm_hier_norm_chunk(const void *qw, const void *si, const void *sb,
+                                      const void *x, const void *bias, void *y, int32_t in_f,
+                                      int32_t out_f, int32_t n, int32_t accum,
+                                      const void *norm_w, float eps, void *h_out);
+/* wst_gemm_int4_hier(qkv weights, x -> qkv, bias) + wst_rope_cache_chunk:
+ * qkv f32 [n][(n_q+2*n_kv)*head_dim] ends as the unfused pair leaves it
+ * (q rotated, k and v as computed), k/v rows appended to the caches at
+ * pos0 .. pos0+n-1; head_dim <= 128. */
+wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si, const void *sb,
+                                      const void *x, const void *bias, void *qkv, int32_t in_f,
+                                      void *k_cache, void *v_cache, const void *cos_tab,
+                                      const void *sin_tab, int32_t n_q, int32_t n_kv,
+                                      int32_t head_dim, int32_t pos0, int32_t n,
+                                      int32_t max_seq, const void *q_norm_w,
+                                      const void *k_norm_w, float eps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,7 +55,7 @@ struct wse_engine {
   // chunk scratch, allocated on first use
   int chunk_width = 0;
   void *c_tokens = nullptr, *c_x = nullptr, *c_h = nullptr, *c_qkv = nullptr, *c_attn = nullptr,
-       *c_gu = nullptr, *c_act = nullptr;
+       *c_act = nullptr;
   void *c_logits = nullptr, *c_picks = nullptr;  // the chunk head's, on first use
   void *nll_acc = nullptr;                       // cross_entropy's (sum, count), on first use
   bool c_ran = false;                            // a chunk pass has left picks
@@ -737,7 +737,6 @@ static wst_status_t ensure_chunk(wse_engine *e) {
   TRY(a.alloc(&e->c_h, w * H * 2, true));
   TRY(a.alloc(&e->c_qkv, w * nqkv * 4, true));
   TRY(a.alloc(&e->c_attn, w * (size_t)c.n_q * hd * 2, true));
-  TRY(a.alloc(&e->c_gu, w * 2 * I * 4, true));
   TRY(a.alloc(&e->c_act, w * I * 2, true));
   e->chunk_width = (int)w;
   return WST_OK;
@@ -774,25 +773,44 @@ static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool
   else
     TRY(wst_embed_int4_hier_chunk(m.embed.qw, m.embed.si, m.embed.sb, e->c_tokens, e->c_x, H, V,
                                   n));
+  // Fused chunk forms (whetstone_ext.h; bit-identical to the reference's op
+  // sequence): qkv GEMM + RoPE/KV append, o GEMM + post-attention norm, gate|up
+  // GEMM + SwiGLU, down GEMM + the next norm (the next layer's input norm, or
+  // the final norm before the head). Unfused where a fused form does not
+  // apply (f16 head path aside, head_dim above 128).
+  const bool rope_fused = hd <= 128;
+  TRY(wst_rmsnorm_chunk(e->c_x, m.layers[0].in_norm, e->c_h, H, n, eps));
   for (int l = 0; l < c.n_layers; ++l) {
     const Layer &L = m.layers[(size_t)l];
-    TRY(wst_rmsnorm_chunk(e->c_x, L.in_norm, e->c_h, H, n, eps));
-    TRY(wst_gemm_int4_hier(L.qkv.qw, L.qkv.si, L.qkv.sb, e->c_h, L.qkv_bias, e->c_qkv, H, nqkv, n, 0));
-    TRY(wst_rope_cache_chunk(e->c_qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab, e->sin_tab,
-                             nq, nkv, hd, pos0, n, e->max_seq, L.q_norm, L.k_norm, eps));
+    if (rope_fused) {
+      TRY(wst_gemm_hier_rope_chunk(L.qkv.qw, L.qkv.si, L.qkv.sb, e->c_h, L.qkv_bias, e->c_qkv, H,
+                                   e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab, e->sin_tab, nq,
+                                   nkv, hd, pos0, n, e->max_seq, L.q_norm, L.k_norm, eps));
+    } else {
+      TRY(wst_gemm_int4_hier(L.qkv.qw, L.qkv.si, L.qkv.sb, e->c_h, L.qkv_bias, e->c_qkv, H, nqkv,
+                             n, 0));
+      TRY(wst_rope_cache_chunk(e->c_qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab,
+                               e->sin_tab, nq, nkv, hd, pos0, n, e->max_seq, L.q_norm, L.k_norm,
+                               eps));
+    }
     TRY(wst_attn_chunk(e->c_qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->c_attn, nq, nkv, hd, pos0,
                        n, e->max_seq, scale));
-    TRY(wst_gemm_int4_hier(L.o.qw, L.o.si, L.o.sb, e->c_attn, nullptr, e->c_x, nq * hd, H, n, 1));
-    TRY(wst_rmsnorm_chunk(e->c_x, L.post_norm, e->c_h, H, n, eps));
-    TRY(wst_gemm_int4_hier(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->c_h, nullptr, e->c_gu, H,
-                           2 * I, n, 0));
-    TRY(wst_swiglu_chunk(e->c_gu, e->c_act, I, n));
-    TRY(wst_gemm_int4_hier(L.down.qw, L.down.si, L.down.sb, e->c_act, nullptr, e->c_x, I, H, n, 1));
+    TRY(wst_gemm_hier_norm_chunk(L.o.qw, L.o.si, L.o.sb, e->c_attn, nullptr, e->c_x, nq * hd, H, n,
+                                 1, L.post_norm, eps, e->c_h));
+    TRY(wst_gemm_hier_swiglu_chunk(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->c_h, e->c_act, H,
+                                   I, n));
+    const bool last = l + 1 == c.n_layers;
+    if (!last || want_logits)
+      TRY(wst_gemm_hier_norm_chunk(L.down.qw, L.down.si, L.down.sb, e->c_act, nullptr, e->c_x, I,
+                                   H, n, 1, last ? m.final_norm : m.layers[(size_t)l + 1].in_norm,
+                                   eps, e->c_h));
+    else
+      TRY(wst_gemm_int4_hier(L.down.qw, L.down.si, L.down.sb, e->c_act, nullptr, e->c_x, I, H, n,
+                             1));
   }
   if (want_logits) {
     const Mat &head = m.head();
     TRY(ensure_chunk_head(e));
-    TRY(wst_rmsnorm_chunk(e->c_x, m.final_norm, e->c_h, H, n, eps));
     if (head.dense())
       TRY(wst_gemm_fp16(head.w16, e->c_h, nullptr, e->c_logits, H, V, n, 0));
     else

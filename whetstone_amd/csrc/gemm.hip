@@ -67,7 +67,10 @@ struct GmStage {
 // HIER: w = (qw, si, sb) int4-hier-g32; else w is f16 [out_f][in_f].
 // Split z = blockIdx.z covers groups [z*gps, min(G, (z+1)*gps)); with one
 // split the epilogue writes y, otherwise the f32 tile goes to ws[z].
-template <bool HIER>
+// SWI: the gate|up form. Tile row k < 32 is gate row a0 + k and row 32 + k is
+// up row inter + a0 + k (a0 = 32 * blockIdx.x, out_f = inter), and the
+// epilogue writes act[tok][a0 + k] = f16(silu(gate) * up) (never split).
+template <bool HIER, bool SWI>
 __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
     const void *__restrict__ w, const uint8_t *__restrict__ si, const uint32_t *__restrict__ sb,
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ bias, float *__restrict__ y,
@@ -83,7 +86,8 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 
   // W assignment: row wr = tid / 4, group wg = tid % 4 of the step.
   const int wr = tid >> 2, wg = tid & 3;
-  const int wrow = min(r0 + wr, out_f - 1);
+  const int wrow = SWI ? (wr < 32 ? min(r0 / 2 + wr, out_f - 1) : out_f + min(r0 / 2 + wr - 32, out_f - 1))
+                      : min(r0 + wr, out_f - 1);
   float d = 0.0f, dm = 0.0f;
   if constexpr (HIER) {
     const uint32_t p = sb[wrow];
@@ -209,7 +213,34 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
       for (int i = 0; i < 4; ++i)
         ct[(wave * 32 + b * 16 + r16) * GM_CS + a * 16 + (lane >> 4) * 4 + i] = acc[a][b][i];
   __syncthreads();
-  const bool split = gridDim.z > 1;
+  if constexpr (SWI) {
+    // act[tok][a0 + k] for k < 32: the same expression as swiglu_kernel.
+    uint16_t *act = (uint16_t *)y;
+    const int a0 = r0 / 2;
+#pragma unroll
+    for (int j = 0; j < GM_BN * 32 / 4 / GM_THREADS; ++j) {
+      const int idx = tid + GM_THREADS * j;
+      const int tl = idx / 8, kl = (idx % 8) * 4;
+      const int tok = t0 + tl;
+      if (tok >= n) continue;
+      uint16_t hv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float g = ct[tl * GM_CS + kl + e], u = ct[tl * GM_CS + 32 + kl + e];
+        hv[e] = f2h(g / (1.0f + __expf(-g)) * u);
+      }
+      uint16_t *dst = act + (size_t)tok * out_f + a0 + kl;
+      if ((out_f & 3) == 0 && a0 + kl + 3 < out_f) {
+        *(uint2 *)dst = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (a0 + kl + e < out_f) dst[e] = hv[e];
+      }
+    }
+    return;
+  }
+  const bool split = gridDim.z > 1 || ws;
   float *dst0 = split ? ws + (size_t)blockIdx.z * n * out_f : y;
   const bool vec = (out_f & 3) == 0;
 #pragma unroll
@@ -241,6 +272,20 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
   }
 }
 
+// sum over the splits of element i (stride `total`), in split order: the
+// loads are issued together (up to GM_MAXSPLIT), the adds stay in order.
+#define GM_MAXSPLIT 16
+__device__ __forceinline__ float split_sum(const float *__restrict__ ws, size_t i, size_t total,
+                                           int splits) {
+  float v[GM_MAXSPLIT];
+#pragma unroll
+  for (int z = 0; z < GM_MAXSPLIT; ++z) v[z] = ws[(size_t)min(z, splits - 1) * total + i];
+  float t = v[0];
+#pragma unroll
+  for (int z = 1; z < GM_MAXSPLIT; ++z) t = z < splits ? t + v[z] : t;
+  return t;
+}
+
 // y = (accum ? y : 0) + (sum of the splits in split order) + bias.
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float *__restrict__ ws,
                                                                 const uint16_t *__restrict__ bias,
@@ -248,33 +293,148 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float *__r
                                                                 int n, int splits, int accum) {
   const size_t total = (size_t)n * out_f;
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
-    float v = ws[i];
-    for (int z = 1; z < splits; ++z) v += ws[(size_t)z * total + i];
+    float v = split_sum(ws, i, total, splits);
     if (bias) v += h2f(bias[i % out_f]);
     y[i] = accum ? y[i] + v : v;
   }
 }
 
-wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void *sb,
-                           const void *x, const void *bias, void *y, int32_t in_f, int32_t out_f,
-                           int32_t n, int32_t accum) {
-  static bool attr[2] = {false, false};
-  if (!attr[hier]) {
-    const void *k = hier ? (const void *)gemm_mfma_kernel<true> : (const void *)gemm_mfma_kernel<false>;
-    (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS);
-    attr[hier] = true;
+// Fused reduce + RMSNorm (a token per 512-thread block): x = (accum ? x : 0) +
+// (sum of the splits in split order) + bias, staged in LDS, then
+// h = f16(x * rms * w) with rms_scale512's order, so both outputs equal
+// gemm_split_reduce_kernel followed by rmsnorm_kernel bit for bit.
+__global__ __launch_bounds__(512) void gemm_reduce_norm_kernel(
+    const float *__restrict__ ws, const uint16_t *__restrict__ bias, float *__restrict__ y,
+    int out_f, int n, int splits, int accum, const uint16_t *__restrict__ nw, float eps,
+    uint16_t *__restrict__ h) {
+  __shared__ float red[16];
+  extern __shared__ float xrow[];  // [out_f]: the reduced row
+  const int tok = blockIdx.x;
+  const size_t total = (size_t)n * out_f, base = (size_t)tok * out_f;
+  // 1. the reduce, coalesced (thread t: elements t, t+512, ...)
+  for (int c = threadIdx.x; c < out_f; c += 512) {
+    float t = split_sum(ws, base + c, total, splits);
+    if (bias) t += h2f(bias[c]);
+    t = accum ? y[base + c] + t : t;
+    y[base + c] = t;
+    xrow[c] = t;
   }
+  __syncthreads();
+  // 2. the RMS in rms_scale512's order, from LDS
+  const float sc = rms_scale512(xrow, out_f, eps, red);
+  // 3. h, coalesced
+  for (int c = threadIdx.x; c < out_f; c += 512)
+    h[base + c] = f2h(xrow[c] * sc * h2f(nw[c]));
+}
+
+// Fused reduce + QK-norm + RoPE + KV append, one 64-thread block per (head,
+// token) as rope_cache_kernel (head_dim <= 128, so a head's halves are one
+// wave): the head's qkv values are summed from the splits (+ bias) exactly as
+// gemm_split_reduce_kernel does and stored to qkv, then rotated exactly as
+// rope_cache_kernel does (q back into qkv, k and v to the cache).
+__global__ __launch_bounds__(64) void gemm_reduce_rope_kernel(
+    const float *__restrict__ ws, const uint16_t *__restrict__ bias, float *__restrict__ qkv,
+    int splits, int n, uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache,
+    const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, int n_q, int n_kv,
+    int hd, int pos0, int max_seq, const uint16_t *__restrict__ q_norm_w,
+    const uint16_t *__restrict__ k_norm_w, float eps) {
+  __shared__ float red[16];
+  const int head = blockIdx.x, tok = blockIdx.y;
+  const int half = hd >> 1, j = threadIdx.x;
+  const bool active = j < half;
+  const int nqkv = (n_q + 2 * n_kv) * hd;
+  const size_t total = (size_t)n * nqkv;
+  float *row = qkv + (size_t)tok * nqkv;
+  const float *wrow = ws + (size_t)tok * nqkv;
+  auto red_at = [&](int c) {  // the split sum of column c (stored to qkv)
+    float t = split_sum(wrow, c, total, splits);
+    if (bias) t += h2f(bias[c]);
+    row[c] = t;
+    return t;
+  };
+  const int pos = min(max(pos0 + tok, 0), max_seq - 1);
+  const float c = active ? cos_tab[(size_t)pos * half + j] : 0.0f;
+  const float s = active ? sin_tab[(size_t)pos * half + j] : 0.0f;
+  if (head < n_q) {
+    const int q0 = head * hd;
+    float x1 = active ? red_at(q0 + j) : 0.0f;
+    float x2 = active ? red_at(q0 + j + half) : 0.0f;
+    if (q_norm_w) qk_norm(x1, x2, q_norm_w, j, half, hd, eps, active, red);
+    if (!active) return;
+    row[q0 + j] = rope_lo(x1, x2, c, s);
+    row[q0 + j + half] = rope_hi(x1, x2, c, s);
+    return;
+  }
+  const int kvh = head - n_q;
+  const int k0 = (n_q + kvh) * hd, v0 = (n_q + n_kv + kvh) * hd;
+  float k1 = active ? red_at(k0 + j) : 0.0f;
+  float k2 = active ? red_at(k0 + j + half) : 0.0f;
+  const float va = active ? red_at(v0 + j) : 0.0f;
+  const float vb = active ? red_at(v0 + j + half) : 0.0f;
+  if (k_norm_w) qk_norm(k1, k2, k_norm_w, j, half, hd, eps, active, red);
+  if (!active) return;
+  const size_t slot = ((size_t)kvh * max_seq + pos) * hd;
+  k_cache[slot + j] = f2h(rope_lo(k1, k2, c, s));
+  k_cache[slot + j + half] = f2h(rope_hi(k1, k2, c, s));
+  v_cache[slot + j] = f2h(va);
+  v_cache[slot + j + half] = f2h(vb);
+}
+
+namespace {
+template <bool HIER, bool SWI>
+void set_lds_attr() {
+  static bool done = false;
+  if (!done) {
+    (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<HIER, SWI>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS);
+    done = true;
+  }
+}
+
+// Splits so that the grid covers the chip, each at least one step long.
+void plan_splits(int in_f, int out_f, int n, int *splits, int *gps) {
   const int G = in_f / HGROUP;
   const int tiles = ((out_f + GM_BM - 1) / GM_BM) * ((n + GM_BN - 1) / GM_BN);
-  // Splits so that the grid covers the chip, each at least one step long.
-  int splits = 1, gps = G;
+  *splits = 1;
+  *gps = G;
   const int target = wst_cu_count();
   if (tiles < target / 2) {
     const int want = (target + tiles - 1) / tiles;
-    gps = (G + want - 1) / want;
-    gps = (gps + GM_KG - 1) / GM_KG * GM_KG;
-    splits = (G + gps - 1) / gps;
+    int g = (G + want - 1) / want;
+    g = (g + GM_KG - 1) / GM_KG * GM_KG;
+    if ((G + g - 1) / g > GM_MAXSPLIT) g = (G + GM_MAXSPLIT - 1) / GM_MAXSPLIT;
+    g = (g + GM_KG - 1) / GM_KG * GM_KG;
+    *gps = g;
+    *splits = (G + g - 1) / g;
   }
+}
+
+// The GEMM into the split scratch (always, even with one split): the fused
+// reduce kernels read it.
+wst_status_t gemm_to_scratch(const void *w, const void *si, const void *sb, const void *x,
+                             int in_f, int out_f, int n, float **ws_out, int *splits_out) {
+  set_lds_attr<true, false>();
+  int splits, gps;
+  plan_splits(in_f, out_f, n, &splits, &gps);
+  float *ws = (float *)wst_static_scratch(WST_SCRATCH_GEMM, (size_t)splits * n * out_f * 4);
+  if (!ws) return WST_ERR_OOM;
+  const dim3 grid((out_f + GM_BM - 1) / GM_BM, (n + GM_BN - 1) / GM_BN, splits);
+  gemm_mfma_kernel<true, false><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
+      w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x, nullptr, nullptr, ws,
+      in_f, out_f, n, 0, gps);
+  *ws_out = ws;
+  *splits_out = splits;
+  return WST_OK;
+}
+}  // namespace
+
+wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void *sb,
+                           const void *x, const void *bias, void *y, int32_t in_f, int32_t out_f,
+                           int32_t n, int32_t accum) {
+  if (hier) set_lds_attr<true, false>();
+  else set_lds_attr<false, false>();
+  int splits, gps;
+  plan_splits(in_f, out_f, n, &splits, &gps);
   float *ws = nullptr;
   if (splits > 1) {
     ws = (float *)wst_static_scratch(WST_SCRATCH_GEMM, (size_t)splits * n * out_f * 4);
@@ -282,11 +442,11 @@ wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void 
   }
   const dim3 grid((out_f + GM_BM - 1) / GM_BM, (n + GM_BN - 1) / GM_BN, splits);
   if (hier)
-    gemm_mfma_kernel<true><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
+    gemm_mfma_kernel<true, false><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
         w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
         (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, gps);
   else
-    gemm_mfma_kernel<false><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
+    gemm_mfma_kernel<false, false><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
         w, nullptr, nullptr, (const uint16_t *)x, (const uint16_t *)bias, (float *)y, ws, in_f,
         out_f, n, accum, gps);
   if (splits > 1) {
@@ -295,5 +455,93 @@ wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void 
     gemm_split_reduce_kernel<<<blocks, 256, 0, WST_STREAM>>>(ws, (const uint16_t *)bias,
                                                               (float *)y, out_f, n, splits, accum);
   }
+  return WST_OK;
+}
+
+static wst_status_t chunk_gemm_args(const void *qw, const void *si, const void *sb, const void *x,
+                                    int32_t in_f, int32_t out_f, int32_t n, const char *who) {
+  if (!(qw && si && sb && x)) {
+    snprintf(wst_err_buf, sizeof(wst_err_buf), "%s: null pointer", who);
+    return WST_ERR_INVALID_ARG;
+  }
+  if (in_f <= 0 || out_f <= 0 || n <= 0 || in_f % HGROUP != 0) {
+    snprintf(wst_err_buf, sizeof(wst_err_buf), "%s: bad shape", who);
+    return WST_ERR_INVALID_ARG;
+  }
+  if (((uintptr_t)qw | (uintptr_t)x) & 15u) {
+    snprintf(wst_err_buf, sizeof(wst_err_buf), "%s: qw and x must be 16-byte aligned", who);
+    return WST_ERR_INVALID_ARG;
+  }
+  return WST_OK;
+}
+
+extern "C" wst_status_t wst_gemm_hier_swiglu_chunk(const void *qw, const void *si,
+                                                   const void *sb, const void *x, void *act,
+                                                   int32_t in_f, int32_t inter, int32_t n) {
+  wst_status_t st = chunk_gemm_args(qw, si, sb, x, in_f, inter, n, "wst_gemm_hier_swiglu_chunk");
+  if (st != WST_OK) return st;
+  WST_REQUIRE(act, "wst_gemm_hier_swiglu_chunk: null pointer");
+  set_lds_attr<true, true>();
+  const dim3 grid((inter + 31) / 32, (n + GM_BN - 1) / GM_BN, 1);
+  gemm_mfma_kernel<true, true><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
+      qw, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x, nullptr, (float *)act,
+      nullptr, in_f, inter, n, 0, in_f / HGROUP);
+  WST_TRY_KERNEL("wst_gemm_hier_swiglu_chunk");
+  return WST_OK;
+}
+
+extern "C" wst_status_t wst_gemm_hier_norm_chunk(const void *qw, const void *si, const void *sb,
+                                                const void *x, const void *bias, void *y,
+                                                int32_t in_f, int32_t out_f, int32_t n,
+                                                int32_t accum, const void *norm_w, float eps,
+                                                void *h_out) {
+  wst_status_t st = chunk_gemm_args(qw, si, sb, x, in_f, out_f, n, "wst_gemm_hier_norm_chunk");
+  if (st != WST_OK) return st;
+  WST_REQUIRE(y && norm_w && h_out, "wst_gemm_hier_norm_chunk: null pointer");
+  WST_REQUIRE(out_f <= 16384, "wst_gemm_hier_norm_chunk: out_features above 16384");
+  float *ws;
+  int splits;
+  st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits);
+  if (st != WST_OK) return st;
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void *)gemm_reduce_norm_kernel,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4);
+    attr = true;
+  }
+  gemm_reduce_norm_kernel<<<n, 512, (size_t)out_f * 4, WST_STREAM>>>(ws, (const uint16_t *)bias, (float *)y, out_f,
+                                                     n, splits, accum, (const uint16_t *)norm_w,
+                                                     eps, (uint16_t *)h_out);
+  WST_TRY_KERNEL("wst_gemm_hier_norm_chunk");
+  return WST_OK;
+}
+
+extern "C" wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si, const void *sb,
+                                                const void *x, const void *bias, void *qkv,
+                                                int32_t in_f, void *k_cache, void *v_cache,
+                                                const void *cos_tab, const void *sin_tab,
+                                                int32_t n_q, int32_t n_kv, int32_t head_dim,
+                                                int32_t pos0, int32_t n, int32_t max_seq,
+                                                const void *q_norm_w, const void *k_norm_w,
+                                                float eps) {
+  WST_REQUIRE(n_q > 0 && n_kv > 0 && head_dim > 0 && n > 0 && n <= 65535,
+              "wst_gemm_hier_rope_chunk: bad shape");
+  WST_REQUIRE(head_dim % 2 == 0 && head_dim <= 128, "wst_gemm_hier_rope_chunk: head_dim above 128");
+  const int out_f = (n_q + 2 * n_kv) * head_dim;
+  wst_status_t st = chunk_gemm_args(qw, si, sb, x, in_f, out_f, n, "wst_gemm_hier_rope_chunk");
+  if (st != WST_OK) return st;
+  WST_REQUIRE(qkv && k_cache && v_cache && cos_tab && sin_tab,
+              "wst_gemm_hier_rope_chunk: null pointer");
+  WST_REQUIRE(max_seq > 0 && pos0 >= 0 && pos0 + n <= max_seq,
+              "wst_gemm_hier_rope_chunk: chunk does not fit the cache");
+  float *ws;
+  int splits;
+  st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits);
+  if (st != WST_OK) return st;
+  gemm_reduce_rope_kernel<<<dim3(n_q + n_kv, n), 64, 0, WST_STREAM>>>(
+      ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,
+      (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv, head_dim,
+      pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
+  WST_TRY_KERNEL("wst_gemm_hier_rope_chunk");
   return WST_OK;
 }
