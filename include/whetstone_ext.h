@@ -98,7 +98,9 @@ wst_status_t wst_head_rescore_fused(const void *head, const void *x, void *logit
  *
  * wst_gemm_int4_hier(gate|up, x -> gu [n][2*inter]) + wst_swiglu_chunk(gu ->
  * act): act f16 [n][inter]; qw/si/sb are the fused gate|up matrix
- * [2*inter][in_f] (gate rows first). */
+ * [2*inter][in_f] (gate rows first). It never splits K, so where the unfused
+ * GEMM would (outputs too few to fill the chip) the f32 sums are added in
+ * another order and act may differ in the last place. */
 wst_status_t wst_gemm_hier_swiglu_chunk(const void *qw, const void *si, const void *sb,
                                         const void *x, void *act, int32_t in_f, int32_t inter,
                                         int32_t n);
