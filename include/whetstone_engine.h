@@ -177,6 +177,45 @@ wst_status_t wse_speculate_generate(wse_engine_t *e, const int32_t *prompt_host,
                                     int32_t max_new, const wse_spec_config_t *cfg,
                                     int32_t *out_tokens_host, int32_t *n_out,
                                     wse_spec_stats_t *stats);
+/* SamplingConfig (engine.rs:104-124). temperature <= 0 means greedy; top_p >= 1,
+ * top_k = 0, min_p = 0 and repeat_penalty = 1 each disable their filter. */
+typedef struct {
+  float temperature;
+  float top_p;
+  int32_t top_k;
+  float min_p;
+  float repeat_penalty;
+  int32_t repeat_last_n;
+  uint64_t seed;
+} wse_sampling_config_t;
+/* sample_with (engine.rs:987-1096), host only: repetition penalty over the last
+ * repeat_last_n of recent[0..n_recent) (oldest first; applied in place to
+ * logits, once per occurrence), then argmax (ties to the last maximum) when
+ * temperature <= 0, else a pool of the top min(top_k or 512, 512) logits
+ * (equal logits ordered by index, where the reference leaves it unspecified),
+ * temperature, min-p, top-p and one draw with
+ * u = splitmix64(seed ^ step * 0x9E3779B97F4A7C15) / 2^64 * mass. */
+int32_t wse_sample_with(float *logits, int32_t n, const wse_sampling_config_t *cfg,
+                        uint64_t step, const int32_t *recent, int32_t n_recent);
+uint64_t wse_splitmix64(uint64_t z);
+/* Engine::sample (engine.rs:648-673): cfg NULL is Sampler::Greedy (the device
+ * cursor's token, a 4-byte read); otherwise the logits come to the host, are
+ * sampled with the engine's recent-token window (the last 2048 tokens fed or
+ * chosen since the last reset), and the choice is written to the device
+ * cursor. The chosen token joins the window. */
+wst_status_t wse_engine_sample(wse_engine_t *e, const wse_sampling_config_t *cfg, uint64_t step,
+                               int32_t *out);
+/* Engine::generate with a sampler (engine.rs:909-956): prefill, then
+ * next = sample(0); for each step: emit next, stop at the cache end, step,
+ * next = sample(step + 1). Writes up to n_new tokens and their count. */
+wst_status_t wse_engine_generate_sampled(wse_engine_t *e, const int32_t *prompt_host,
+                                         int32_t n_prompt, int32_t n_new, int32_t chunked,
+                                         const wse_sampling_config_t *cfg,
+                                         int32_t *out_tokens_host, int32_t *n_out);
+/* The recent-token window (oldest first): writes up to cap tokens, returns
+ * the window's length. Engine::unnote (engine.rs:462-467) drops the last k. */
+int32_t wse_engine_recent(const wse_engine_t *e, int32_t *out, int32_t cap);
+void wse_engine_unnote(wse_engine_t *e, int32_t k);
 /* Writes `token` into the device token cursor (the next step's input). */
 wst_status_t wse_engine_set_token(wse_engine_t *e, int32_t token);
 wst_status_t wse_engine_logits(wse_engine_t *e, float *out_host);

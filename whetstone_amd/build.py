@@ -56,7 +56,7 @@ LIB_SOURCES = [
     "chunk.hip",
     "stubs.hip",
 ]
-ENGINE_SOURCES = ["engine.cpp", "wstone.cpp", "speculate.cpp"]
+ENGINE_SOURCES = ["engine.cpp", "wstone.cpp", "speculate.cpp", "sampler.cpp"]
 
 
 def hipcc() -> str:

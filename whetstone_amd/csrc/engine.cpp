@@ -12,6 +12,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <deque>
 #include <string>
 #include <vector>
 
@@ -58,6 +59,7 @@ struct wse_engine {
        *c_act = nullptr;
   void *c_logits = nullptr, *c_picks = nullptr;  // the chunk head's, on first use
   void *nll_acc = nullptr;                       // cross_entropy's (sum, count), on first use
+  std::deque<int32_t> recent;                    // repetition-penalty window (RECENT_CAP)
   bool c_ran = false;                            // a chunk pass has left picks
   std::vector<void *> events;
   Arena arena;
@@ -363,7 +365,33 @@ wst_status_t wse_engine_set_pos(wse_engine_t *e, int32_t pos) {
   return wst_memcpy_h2d(e->pos_dev, &pos, 4);
 }
 
-wst_status_t wse_engine_reset(wse_engine_t *e) { return wse_engine_set_pos(e, 0); }
+// Engine::reset (engine.rs:434-439): position zero and an empty window.
+wst_status_t wse_engine_reset(wse_engine_t *e) {
+  if (!e) return WST_ERR_INVALID_ARG;
+  e->recent.clear();
+  return wse_engine_set_pos(e, 0);
+}
+
+// Engine::note (engine.rs:469-474): the last RECENT_CAP = 2048 tokens.
+static void note(wse_engine *e, int32_t t) {
+  if (e->recent.size() == 2048) e->recent.pop_front();
+  e->recent.push_back(t);
+}
+
+void wse_engine_unnote(wse_engine_t *e, int32_t k) {
+  if (!e) return;
+  for (int32_t i = 0; i < k && !e->recent.empty(); ++i) e->recent.pop_back();
+}
+
+int32_t wse_engine_recent(const wse_engine_t *e, int32_t *out, int32_t cap) {
+  if (!e) return 0;
+  int32_t i = 0;
+  for (int32_t t : e->recent) {
+    if (out && i < cap) out[i] = t;
+    ++i;
+  }
+  return i;
+}
 
 wst_status_t wse_engine_fill_kv(wse_engine_t *e, uint64_t seed, int32_t n) {
   if (!e || n < 0 || n > e->max_seq) return WST_ERR_INVALID_ARG;
@@ -518,6 +546,7 @@ wst_status_t wse_engine_forward(wse_engine_t *e, int32_t token) {
   if (!e) return WST_ERR_INVALID_ARG;
   TRY(check_room(e));
   TRY(wst_memcpy_h2d(e->token, &token, 4));
+  note(e, token);
   return wse_engine_step(e);
 }
 
@@ -821,6 +850,7 @@ static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool
     TRY(wst_memcpy_d2d(e->token, (const char *)e->c_picks + (size_t)(n - 1) * 4, 4));
     e->c_ran = true;
   }
+  for (int i = 0; i < n; ++i) note(e, ids[i]);
   return wse_engine_set_pos(e, pos0 + n);
 }
 
@@ -899,11 +929,54 @@ wst_status_t wse_engine_generate(wse_engine_t *e, const int32_t *prompt, int32_t
   TRY(wse_engine_prefill(e, prompt, n_prompt, chunked));
   int32_t next = 0;
   TRY(wse_engine_token(e, &next));
+  note(e, next);  // Sampler::Greedy notes its pick (engine.rs:650-656)
   for (int i = 0; i < n_new; ++i) {
     out[i] = next;
     if (i + 1 == n_new || e->pos >= e->max_seq) break;
     TRY(wse_engine_step(e));
     TRY(wse_engine_token(e, &next));
+    note(e, next);
+  }
+  return WST_OK;
+}
+
+wst_status_t wse_engine_sample(wse_engine_t *e, const wse_sampling_config_t *cfg, uint64_t step,
+                               int32_t *out) {
+  if (!e || !out) return WST_ERR_INVALID_ARG;
+  int32_t t = 0;
+  if (!cfg) {
+    TRY(wse_engine_token(e, &t));
+  } else {
+    std::vector<float> lg((size_t)e->m->c.vocab);
+    TRY(wse_engine_logits(e, lg.data()));
+    std::vector<int32_t> rc(e->recent.begin(), e->recent.end());
+    t = wse_sample_with(lg.data(), e->m->c.vocab, cfg, step, rc.data(), (int32_t)rc.size());
+    TRY(wse_engine_set_token(e, t));
+  }
+  note(e, t);
+  *out = t;
+  return WST_OK;
+}
+
+wst_status_t wse_engine_generate_sampled(wse_engine_t *e, const int32_t *prompt, int32_t n_prompt,
+                                         int32_t n_new, int32_t chunked,
+                                         const wse_sampling_config_t *cfg, int32_t *out,
+                                         int32_t *n_out) {
+  if (!e || !prompt || n_new < 0 || (n_new && !out) || !n_out) return WST_ERR_INVALID_ARG;
+  *n_out = 0;
+  if (n_prompt <= 0) {
+    snprintf(g_msg, sizeof(g_msg), "cannot generate from an empty prompt");
+    return WST_ERR_SHAPE;
+  }
+  TRY(wse_engine_prefill(e, prompt, n_prompt, chunked));
+  int32_t next = 0;
+  TRY(wse_engine_sample(e, cfg, 0, &next));
+  for (int32_t st = 0; st < n_new; ++st) {
+    out[st] = next;
+    *n_out = st + 1;
+    if (e->pos >= e->max_seq) break;
+    TRY(wse_engine_step(e));
+    TRY(wse_engine_sample(e, cfg, (uint64_t)st + 1, &next));
   }
   return WST_OK;
 }

@@ -111,6 +111,7 @@ wst_status_t wse_speculate_generate(wse_engine_t *e, const int32_t *prompt, int3
     st.accepted += m;
     // The cache keeps inputs[0..=m]; the rejected tail is overwritten later.
     TRY(wse_engine_rewind(e, pos0 + m + 1));
+    wse_engine_unnote(e, k - (m + 1));  // speculate.rs:240: the rejected inputs leave the window
     bool stop = false;
     for (int j = 1; j <= m; ++j) {
       out_tokens[generated++] = inputs[(size_t)j];

@@ -77,6 +77,12 @@ _SIG = {
     "wse_engine_forward_chunk": (I32, [P, P, I32, I32]),
     "wse_engine_chunk_picks": (I32, [P, I32, P]),
     "wse_engine_rewind": (I32, [P, I32]),
+    "wse_sample_with": (I32, [P, I32, P, C.c_uint64, P, I32]),
+    "wse_splitmix64": (C.c_uint64, [C.c_uint64]),
+    "wse_engine_sample": (I32, [P, P, C.c_uint64, C.POINTER(I32)]),
+    "wse_engine_generate_sampled": (I32, [P, P, I32, I32, I32, P, P, C.POINTER(I32)]),
+    "wse_engine_recent": (I32, [P, P, I32]),
+    "wse_engine_unnote": (None, [P, I32]),
     "wse_engine_cross_entropy": (I32, [P, P, C.c_int64, I32, I32, C.POINTER(C.c_double),
                                        C.POINTER(C.c_int64)]),
     "wse_spec_propose": (I32, [P, I32, I32, I32, I32, P]),
@@ -90,6 +96,30 @@ class SpecConfig(C.Structure):
 
     def __init__(self, draft: int = 4, ngram_max: int = 3, ngram_min: int = 2):
         super().__init__(draft, ngram_max, ngram_min)
+
+
+class SamplingConfig(C.Structure):
+    """SamplingConfig (engine.rs:104-137); the defaults are the reference's."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", I32),
+                ("min_p", C.c_float), ("repeat_penalty", C.c_float), ("repeat_last_n", I32),
+                ("seed", C.c_uint64)]
+
+    def __init__(self, temperature=0.7, top_p=0.8, top_k=20, min_p=0.0, repeat_penalty=1.05,
+                 repeat_last_n=64, seed=0):
+        super().__init__(temperature, top_p, top_k, min_p, repeat_penalty, repeat_last_n, seed)
+
+
+def sample_with(logits, cfg: "SamplingConfig", step: int, recent=()):
+    """sample_with on a host copy: (token, the penalised logits)."""
+    v = np.array(logits, np.float32, copy=True)
+    r = np.ascontiguousarray(list(recent), np.int32)
+    t = lib().wse_sample_with(v.ctypes.data, v.size, C.byref(cfg), step,
+                              r.ctypes.data if r.size else None, r.size)
+    return int(t), v
+
+
+def splitmix64(z: int) -> int:
+    return int(lib().wse_splitmix64(z))
 
 
 class SpecStats(C.Structure):
@@ -306,6 +336,30 @@ class Engine:
         _check(lib().wse_engine_cross_entropy(self.h, a.ctypes.data, a.size, window, max_windows,
                                               C.byref(nll), C.byref(n)))
         return nll.value, n.value
+
+    def sample(self, cfg: "SamplingConfig | None", step: int) -> int:
+        """Engine::sample: None is Sampler::Greedy."""
+        t = C.c_int32()
+        _check(lib().wse_engine_sample(self.h, C.byref(cfg) if cfg is not None else None, step,
+                                       C.byref(t)))
+        return t.value
+
+    def generate_sampled(self, prompt, n_new: int, cfg: "SamplingConfig | None",
+                         chunked: bool = True) -> np.ndarray:
+        a = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(n_new, 1), np.int32)
+        n = C.c_int32()
+        _check(lib().wse_engine_generate_sampled(self.h, a.ctypes.data, a.size, n_new,
+                                                 int(chunked),
+                                                 C.byref(cfg) if cfg is not None else None,
+                                                 out.ctypes.data, C.byref(n)))
+        return out[:n.value]
+
+    def recent(self) -> list:
+        n = lib().wse_engine_recent(self.h, None, 0)
+        out = np.zeros(max(n, 1), np.int32)
+        lib().wse_engine_recent(self.h, out.ctypes.data, n)
+        return [int(v) for v in out[:n]]
 
     def set_token(self, token: int):
         _check(lib().wse_engine_set_token(self.h, token))
