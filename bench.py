@@ -21,6 +21,8 @@ The line printed carries:
 
     python bench.py [--steps 256] [--warmup 8] [--config 3|2] [--cpu-seconds 12]
 
+`--config 1` measures the GEMV alone (lm_head and 0.5B block shapes, weights
+cold past the MALL and hot) and prints a line of its own.
 `--config 4` instead measures the chunked prefill (0.5B shape with QK-norm and
 the int4 head rescored from an fp16 copy, top-32): a 4096-token seeded prompt
 in 256-token chunks through the MFMA GEMMs, then 128 greedy decode steps, and
@@ -62,7 +64,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=256)
     p.add_argument("--warmup", type=int, default=8)
-    p.add_argument("--config", type=int, default=3, choices=(2, 3, 4))
+    p.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4))
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline budget (tokens are added until it is spent)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -281,6 +283,67 @@ def prefill_bench(E, wk, n_new: int) -> None:
     print(json.dumps(line), flush=True)
 
 
+def gemv_bench(wk, reps: int) -> None:
+    """Config 1: the int4-hier-g32 GEMV alone, y f32 = W x (x f16 N(0,1), W
+    N(0,0.02) packed on the device), on the 0.5B lm_head shape and the 0.5B
+    block shapes. "cold" cycles through ceil(512 MB / matrix bytes) distinct
+    copies so the 256 MB MALL cannot serve the weights; "hot" repeats one copy.
+    HIP events on the calling thread's stream around `reps` back-to-back
+    launches; bytes per call = packed weights + x + y."""
+    from whetstone_amd import ffi
+    shapes = [("lm_head", 896, 151936), ("qkv", 896, 1152), ("gate_up", 896, 9728),
+              ("down", 4864, 896)]
+    res = {}
+    for name, in_f, out_f in shapes:
+        wbytes = out_f * (in_f // 2 + in_f // 32 + 4)
+        nbytes = wbytes + 2 * in_f + 4 * out_f
+        copies = max(1, -(-512_000_000 // wbytes))
+        qw = wk.DeviceBuffer(copies * out_f * in_f // 2, np.uint8)
+        si = wk.DeviceBuffer(copies * out_f * in_f // 32, np.uint8)
+        sb = wk.DeviceBuffer(copies * out_f * 4, np.uint8)
+        base = (qw.ptr.value, si.ptr.value, sb.ptr.value)
+        ptrs = [(base[0] + c * out_f * in_f // 2, base[1] + c * out_f * in_f // 32,
+                 base[2] + c * out_f * 4) for c in range(copies)]
+        for (q, i_, b) in ptrs:
+            ffi.call("wst_fixture_pack_hier", q, i_, b, in_f, 0, out_f, WEIGHT_SEED, 1, 0.02)
+        x = wk.DeviceBuffer(in_f, np.float16)
+        ffi.call("wst_fixture_normal_f16", x.ptr, in_f, KV_SEED, 2, 0, 1.0, 0.0)
+        y = wk.DeviceBuffer(out_f, np.float32)
+        out = {"in": in_f, "out": out_f, "bytes_per_call": nbytes, "cold_copies": copies}
+        for mode in ("cold", "hot"):
+            seq = ptrs if mode == "cold" else ptrs[:1]
+            for k in range(10):
+                q, i_, b = seq[k % len(seq)]
+                ffi.call("wst_gemv_int4_hier_ex", q, i_, b, x.ptr, None, y.ptr, in_f, out_f, 0)
+            e0, e1 = wk.Event(), wk.Event()
+            e0.record()
+            for k in range(reps):
+                q, i_, b = seq[k % len(seq)]
+                ffi.call("wst_gemv_int4_hier_ex", q, i_, b, x.ptr, None, y.ptr, in_f, out_f, 0)
+            e1.record()
+            wk.synchronize()
+            us = e0.elapsed_ms(e1) * 1e3 / reps
+            out[mode] = {"us_per_call": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+                         "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"{name}: {out}")
+        res[name] = out
+        del qw, si, sb
+    head = res["lm_head"]["cold"]
+    line = {
+        "metric": "int4 hier-g32 GEMV achieved HBM GB/s (config 1: lm_head 896 -> 151936)",
+        "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "int4xf16->f32",
+        "data": "synthetic (seeded N(0,0.02) weights packed to int4-hier-g32 on the device; "
+                "f16 N(0,1) x)",
+        "config": {"workload": "config 1: single int4 hier-g32 GEMV, y[151936] = W x[896], "
+                               "plus the 0.5B block shapes; cold = distinct weight copies "
+                               "cycling past the MALL", "reps": reps, "shapes": res},
+        "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": head["frac"], "traffic": None},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -298,6 +361,9 @@ def main():
                  "and --warmup non-negative")
 
     from whetstone_amd import engine as E, kernels as wk  # raises if not built
+    if a.config == 1:
+        gemv_bench(wk, max(a.steps, 200))
+        return
     if a.config == 4:
         prefill_bench(E, wk, a.steps)
         return

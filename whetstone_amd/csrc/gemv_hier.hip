@@ -115,9 +115,12 @@ __device__ __forceinline__ float group_dot(const uint4 p, const XGroup &xg, uint
   return fmaf(db, 0.0625f, da) - xg.corr;
 }
 
+// Sum over a row's lanes when a row spans LPR <= 64 lanes of one wave (every
+// lane of the row gets the sum).
 template <int LPR>
 __device__ __forceinline__ float slot_sum(float v) {
-  if constexpr (LPR == 32) return half_wave_sum(v);
+  if constexpr (LPR == 16) return dpp_sum16(v);
+  else if constexpr (LPR == 32) return half_wave_sum(v);
   else return wave_sum(v);
 }
 
@@ -145,8 +148,10 @@ __device__ __forceinline__ float slot_sum(float v) {
 // the weight loads ahead of the activation loads.
 //
 // PD: units in flight per row slot (1: the next unit's loads are issued after
-// the current unit's compute; 2: one more unit is always in flight).
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD>
+// the current unit's compute; PD > 1: PD - 1 more units are always in flight).
+// RPW: rows per wave for short rows (WPR == 1): a row is 64 / RPW lanes of a
+// wave, so a wave streams RPW rows at once.
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW = 1>
 __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     const uint4 *qw, const uint8_t *si,
     const uint32_t *__restrict__ sb, const void *xin,
@@ -155,13 +160,14 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     int accum) {
   static_assert(!NORM || NT == NORM_THREADS, "the RMS reduction order assumes 512 threads");
   constexpr int NR = SWIGLU ? 2 : 1;
+  static_assert(RPW == 1 || WPR == 1, "rows share a wave only when a row is one wave or less");
   constexpr int NW = NT / 64;
-  constexpr int RPB = NW / WPR;
-  constexpr int LPR = 64 * WPR;
+  constexpr int RPB = NW / WPR * RPW;
+  constexpr int LPR = WPR > 1 ? 64 * WPR : 64 / RPW;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rs = wave / WPR;
-  const int lr = (wave % WPR) * 64 + lane;
+  const int rs = (wave / WPR) * RPW + (RPW > 1 ? lane / LPR : 0);
+  const int lr = WPR > 1 ? (wave % WPR) * 64 + lane : lane % LPR;
   const int G = in_f / HGROUP, NB8 = in_f / 8;
   __shared__ float red[2][NW][NR];
   __shared__ float bred[16];
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   // return in order, so the table waits only for them); the non-restrict
   // pointers keep the compiler from hoisting the weights above them.
 
-  // 2. the first unit's packed bytes (with PD == 2, the second unit's too)
+  // 2. the first PD units' packed bytes
   const int stride = gridDim.x * RPB;
   int base = blockIdx.x * RPB;
   struct Buf {
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     uint32_t idx[NR][NG];
     uint32_t sbv[NR];
   };
-  Buf b0, b1;
+  Buf bufs[PD];
   auto load_unit = [&](Buf &B, int row) {  // row clamped: past the end loads are unused
     const int rc = min(row, nunits - 1);
 #pragma unroll
@@ -219,8 +225,8 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       }
     }
   };
-  load_unit(b0, base + rs);
-  if constexpr (PD == 2) load_unit(b1, base + stride + rs);
+#pragma unroll
+  for (int i = 0; i < PD; ++i) load_unit(bufs[i], base + i * stride + rs);
 
   // 3. the RMS scale (rms_scale512's order: thread t, blocks t, t+512, ...)
   float s = 1.0f;
@@ -324,7 +330,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     load_unit(B, base + PD * stride + rs);
     float part[NR];
 #pragma unroll
-    for (int k = 0; k < NR; ++k) part[k] = wave_sum(lv[k]);
+    for (int k = 0; k < NR; ++k) part[k] = WPR > 1 ? wave_sum(lv[k]) : slot_sum<LPR>(lv[k]);
     if constexpr (WPR > 1) {
       if (lane == 0)
 #pragma unroll
@@ -340,7 +346,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
         }
       }
     }
-    if (lane == 0 && (wave % WPR) == 0 && row < nunits) {
+    if (lr == 0 && row < nunits) {
       if constexpr (SWIGLU) {
         const float g = part[0], up = part[NR - 1];
         ((uint16_t *)yout)[row] = f2h(g / (1.0f + __expf(-g)) * up);
@@ -353,15 +359,13 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     base += stride;
     ++it;
   };
-  if constexpr (PD == 1) {
-    do process(b0); while (base < nunits);
-  } else {
-    do {
-      process(b0);
-      if (base >= nunits) break;
-      process(b1);
-    } while (base < nunits);
-  }
+  do {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      process(bufs[i]);
+      if (PD > 1 && base >= nunits) break;
+    }
+  } while (base < nunits);
 }
 
 // Fallback for rows wider than GEMV_MAX_G groups: x is re-read from L2 per
@@ -485,9 +489,9 @@ static int gemv_pd_override() {
   return v;
 }
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD>
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW>
 static void launch_pd(const HierArgs &a) {
-  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD>;
+  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW>;
   const size_t lds = (size_t)(a.in_f / HGROUP) * XQ_WORDS * 4;
   // Resident blocks per CU for this instance and LDS size, queried once.
   static thread_local size_t q_lds = (size_t)-1;
@@ -502,7 +506,7 @@ static void launch_pd(const HierArgs &a) {
   // Balanced persistent grid: at most k units per row slot, and just enough
   // blocks that every slot gets k (or k-1), so no tail round runs a fraction
   // of the slots.
-  constexpr int RPB = NT / 64 / WPR;
+  constexpr int RPB = NT / 64 / WPR * RPW;
   const int cap = wst_cu_count() * q_res * RPB;
   const int k = (a.nunits + cap - 1) / cap;
   const int grid = (a.nunits + k * RPB - 1) / (k * RPB);
@@ -512,15 +516,22 @@ static void launch_pd(const HierArgs &a) {
       a.in_f, a.nunits, a.accum);
 }
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU>
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1>
 static void launch_q(const HierArgs &a) {
   int pd = gemv_pd_override();
-  if (pd != 1 && pd != 2) {
-    const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR);
+  if (pd < 1 || pd > 4) {
+    const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR * RPW);
     pd = a.nunits >= 8 * slots ? 2 : 1;
   }
-  if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1>(a);
-  else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2>(a);
+  if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW>(a);
+  else if (pd == 3) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW>(a);
+  else if (pd == 4) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW>(a);
+  else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW>(a);
+}
+
+static int gemv_rpw_override() {
+  const char *e = getenv("WST_GEMV_RPW");
+  return e ? atoi(e) : 0;
 }
 
 // in_f -> (groups per lane, waves per row, activation blocks per thread,
@@ -531,7 +542,16 @@ static void launch_q(const HierArgs &a) {
 template <bool NORM, bool SWIGLU>
 static bool hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
-  if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU>(a);
+  // Rows of at most 32 groups (in_f <= 1024, e.g. the 0.5B hidden 896) share a
+  // wave four at a time: with one row per wave, 28 groups left 36 of 64 lanes
+  // idle and a wave streamed 448 bytes per unit. Measured on the 0.5B lm_head
+  // (151936 x 896): 28.0 us one row per wave, 18.0 two, 15.4 four.
+  // WST_GEMV_RPW=1|2 selects the narrower forms.
+  const int rpw = gemv_rpw_override();
+  if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4>(a);
+  else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2>(a);
+  else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4>(a);
+  else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU>(a);
   else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU>(a);
   else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU>(a);
   else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU>(a);
