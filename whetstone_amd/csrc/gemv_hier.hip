@@ -119,7 +119,8 @@ __device__ __forceinline__ float group_dot(const uint4 p, const XGroup &xg, uint
 // lane of the row gets the sum).
 template <int LPR>
 __device__ __forceinline__ float slot_sum(float v) {
-  if constexpr (LPR == 16) return dpp_sum16(v);
+  if constexpr (LPR == 8) return dpp_sum8(v);
+  else if constexpr (LPR == 16) return dpp_sum16(v);
   else if constexpr (LPR == 32) return half_wave_sum(v);
   else return wave_sum(v);
 }
@@ -543,13 +544,17 @@ template <bool NORM, bool SWIGLU>
 static bool hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
   // Rows of at most 32 groups (in_f <= 1024, e.g. the 0.5B hidden 896) share a
-  // wave four at a time: with one row per wave, 28 groups left 36 of 64 lanes
-  // idle and a wave streamed 448 bytes per unit. Measured on the 0.5B lm_head
-  // (151936 x 896): 28.0 us one row per wave, 18.0 two, 15.4 four.
-  // WST_GEMV_RPW=1|2 selects the narrower forms.
+  // wave: with one row per wave, 28 groups left 36 of 64 lanes idle and a
+  // wave streamed 448 bytes per unit. Measured on the 0.5B lm_head (151936 x
+  // 896, weights cold): 28.0 us one row per wave, 18.0 two, 15.4-16.0 four,
+  // 15.1-15.4 eight (four groups per lane); but eight per wave slows the
+  // latency-bound block GEMVs of that model (config-2 decode 1559 -> 1435
+  // tok/s), so four is the default for every shape (a row's bits must not
+  // depend on the output count). WST_GEMV_RPW=1|2|8 selects the others.
   const int rpw = gemv_rpw_override();
   if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4>(a);
   else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2>(a);
+  else if (G <= 32 && rpw == 8) launch_q<4, 1, 1, 512, NORM, SWIGLU, 8>(a);
   else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4>(a);
   else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU>(a);
   else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU>(a);
