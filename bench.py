@@ -53,6 +53,7 @@ KERNEL_NAMES = {  # kernels each stage launches in the fused step (rocprof names
     "head": "gemv_hier_kernel<NG, WPR, XB, 512, NORM=true, SWIGLU=false, PD>",
 }
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.md"
+GEMV_TRAFFIC_FILE = ROOT / "profiles" / "gemv_cfg1_kernel_trace.md"
 
 
 def log(msg: str) -> None:
@@ -138,14 +139,15 @@ def copy_probe(mib: int) -> None:
     print(json.dumps({"copy_probe_bytes": n, "bandwidth_sweep_gbs": round(gbs, 1)}), flush=True)
 
 
-def traffic_for(config: int, stage: str):
+def traffic_for(config: int, stage: str, path=None):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE,
     scaled by the same counters' reading for a copy of known size; committed
     in profiles/traffic.md as `traffic cfg<N> <stage>: <bytes>` lines."""
-    if not TRAFFIC_FILE.exists():
+    path = path or TRAFFIC_FILE
+    if not path.exists():
         return None
     key = f"traffic cfg{config} {stage}:"
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in path.read_text().splitlines():
         line = line.strip().strip("`")
         if line.startswith(key):
             return int(line[len(key):].strip().split()[0])
@@ -339,7 +341,8 @@ def gemv_bench(wk, reps: int) -> None:
                                "plus the 0.5B block shapes; cold = distinct weight copies "
                                "cycling past the MALL", "reps": reps, "shapes": res},
         "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": head["frac"], "traffic": None},
+                     "unit": "GB/s", "frac": head["frac"],
+                     "traffic": traffic_for(1, "lm_head", GEMV_TRAFFIC_FILE)},
     }
     print(json.dumps(line), flush=True)
 
