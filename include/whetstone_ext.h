@@ -93,6 +93,21 @@ wst_status_t wst_head_rescore_fused(const void *head, const void *x, void *logit
                                     int32_t n, int32_t hidden, int32_t k, int32_t cap,
                                     void *scratch, int32_t nblocks);
 
+/* wst_attn_decode_fused without its merge kernel: the slices' partials are
+ * left for wst_gemv_hier_attn. */
+wst_status_t wst_attn_decode_slices(void *qkv, void *k_cache, void *v_cache,
+                                    const void *cos_tab, const void *sin_tab, void *partials,
+                                    int32_t n_q, int32_t n_kv, int32_t head_dim, const void *pos,
+                                    int32_t max_seq, float scale, const void *q_norm_w,
+                                    const void *k_norm_w, float eps);
+/* The slice merge (attn_merge_kernel) fused into the o GEMV:
+ * y (+)= W merge(partials), with in_f = n_q * head_dim; bit-identical to
+ * wst_attn_decode's merge followed by wst_gemv_int4_hier_ex. head_dim 64 or
+ * 128 and at most 8 slices (max_seq <= 8 * 16384 / head_dim). */
+wst_status_t wst_gemv_hier_attn(const void *qw, const void *si, const void *sb,
+                                const void *partials, void *y, int32_t n_q, int32_t head_dim,
+                                const void *pos, int32_t max_seq, int32_t out_f, int32_t accum);
+
 /* Chunk (prefill) fused forms, each bit-identical to the unfused ABI sequence
  * it replaces (tested so):
  *

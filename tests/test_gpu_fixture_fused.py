@@ -195,3 +195,45 @@ def test_fused_rescore_equals_threshold_compact_rescore(orc, wk):
              rs.scratch.ptr, rs.nblocks)
     assert rs.last_count() <= rs.cap
     assert np.array_equal(l1.numpy().view(np.uint32), l2.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,max_seq,pos,out_f", [(14, 2, 64, 776, 700, 896),
+                                                           (14, 2, 64, 776, 0, 896),
+                                                           (8, 2, 128, 1024, 1023, 512),
+                                                           (28, 4, 128, 600, 257, 3584),
+                                                           (4, 2, 64, 2048, 1500, 96)])
+def test_gemv_hier_attn_equals_merge_then_gemv(orc, wk, n_q, n_kv, hd, max_seq, pos, out_f):
+    """wst_gemv_hier_attn (the slice merge inside the o GEMV) against
+    wst_attn_decode (slices + merge kernel) followed by the plain GEMV, on the
+    same partials: bit for bit, accumulating onto the same y."""
+    from whetstone_amd import ffi
+    rng = np.random.default_rng(pos + 3)
+    kc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
+    vc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
+    q = wk.DeviceBuffer.from_array((rng.standard_normal(n_q * hd) * 2).astype(np.float32))
+    cache = wk.KvCache(n_kv, n_q, hd, max_seq)
+    cache.k.copy_from(kc.view(np.float16))
+    cache.v.copy_from(vc.view(np.float16))
+    cur = wk.DeviceCursor(pos)
+    out = wk.DeviceBuffer(n_q * hd, np.float16)
+    wk.attn_decode(q, cache, out, n_q, cur)
+    in_f = n_q * hd
+    p, _ = orc.quantize(orc.fixture_normal(9, 1, in_f * out_f), in_f, out_f)
+    lin = wk.QuantLinearHier.from_packed(p)
+    y0 = orc.fixture_normal(9, 2, out_f, 1.0)
+    ya, yb = wk.DeviceBuffer.from_array(y0.copy()), wk.DeviceBuffer.from_array(y0.copy())
+    ffi.call("wst_gemv_int4_hier_ex", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, out.ptr, None, ya.ptr,
+             in_f, out_f, 1)
+    ffi.call("wst_gemv_hier_attn", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, cache.partials.ptr,
+             yb.ptr, n_q, hd, cur.buf.ptr, max_seq, out_f, 1)
+    assert np.array_equal(ya.numpy().view(np.uint32), yb.numpy().view(np.uint32))
+
+
+def test_gemv_hier_attn_refuses_long_caches(orc, wk):
+    from whetstone_amd import ffi
+    cache = wk.KvCache(2, 14, 64, 4096)  # 16 slices of 256 positions
+    lin = wk.QuantLinearHier.from_packed(orc.quantize(orc.fixture_normal(9, 1, 896 * 64), 896, 64)[0])
+    y = wk.DeviceBuffer(64, np.float32)
+    with pytest.raises(ffi.WstError):
+        ffi.call("wst_gemv_hier_attn", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, cache.partials.ptr,
+                 y.ptr, 14, 64, wk.DeviceCursor(5).buf.ptr, 4096, 64, 0)

@@ -458,7 +458,7 @@ static void attn_go(const dim3 grid, const void *qkv, void *k_cache, void *v_cac
 template <bool ROPE>
 static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_cache,
                         void *partials, void *out, int n_q, int n_kv, const void *pos,
-                        int max_seq, float scale, const RopeArgs &ra) {
+                        int max_seq, float scale, const RopeArgs &ra, bool merge = true) {
   const int nsplit = attn_slices(head_dim, max_seq);
   const dim3 grid(n_kv, nsplit, attn_head_groups(n_q / n_kv));
   switch (head_dim) {
@@ -475,7 +475,8 @@ static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_ca
                             ra);
       break;
   }
-  attn_merge_kernel<<<dim3(n_q, head_dim / 32), 64, 0, WST_STREAM>>>(
+  if (merge)
+    attn_merge_kernel<<<dim3(n_q, head_dim / 32), 64, 0, WST_STREAM>>>(
       (const float *)partials, (uint16_t *)out, n_q, head_dim, nsplit,
       (const int32_t *)pos, max_seq, ATTN_TILE / head_dim);
 }
@@ -538,5 +539,27 @@ extern "C" wst_status_t wst_attn_decode_fused(void *qkv, void *k_cache, void *v_
   attn_launch<true>(head_dim, qkv, k_cache, v_cache, partials, out, n_q, n_kv, pos, max_seq,
                     scale, ra);
   WST_TRY_KERNEL("wst_attn_decode_fused");
+  return WST_OK;
+}
+
+// wst_attn_decode_fused without the merge: the slices' partials are left for
+// a consumer that merges them itself (wst_gemv_hier_attn).
+extern "C" wst_status_t wst_attn_decode_slices(void *qkv, void *k_cache, void *v_cache,
+                                               const void *cos_tab, const void *sin_tab,
+                                               void *partials, int32_t n_q, int32_t n_kv,
+                                               int32_t head_dim, const void *pos,
+                                               int32_t max_seq, float scale,
+                                               const void *q_norm_w, const void *k_norm_w,
+                                               float eps) {
+  const wst_status_t st =
+      attn_check(qkv, k_cache, v_cache, partials, partials, n_q, n_kv, head_dim, pos, max_seq);
+  if (st != WST_OK) return st;
+  WST_REQUIRE(cos_tab && sin_tab, "wst_attn_decode_slices: null rope table");
+  WST_REQUIRE(head_dim <= 128, "wst_attn_decode_slices: head_dim must be 64 or 128");
+  const RopeArgs ra{(const float *)cos_tab, (const float *)sin_tab, (const uint16_t *)q_norm_w,
+                    (const uint16_t *)k_norm_w, eps};
+  attn_launch<true>(head_dim, qkv, k_cache, v_cache, partials, nullptr, n_q, n_kv, pos, max_seq,
+                    scale, ra, false);
+  WST_TRY_KERNEL("wst_attn_decode_slices");
   return WST_OK;
 }

@@ -449,6 +449,18 @@ static wst_status_t head_logits(wse_engine *e, const void *x_last, bool fused) {
   return wst_gemv_int4_hier_ex(head.qw, head.si, head.sb, e->h, nullptr, e->logits, H, V, 0);
 }
 
+// The fused step merges the attention slices inside the o GEMV (one launch
+// fewer per layer) when the cache has at most 8 slices of 16384 / head_dim
+// positions; WSE_MERGE_IN_O=0 keeps the separate merge kernel.
+static bool merge_in_o(const wse_engine *e) {
+  const int hd = e->m->c.head_dim;
+  if (e->mode != WSE_STEP_FUSED || (hd != 64 && hd != 128)) return false;
+  const char *v = getenv("WSE_MERGE_IN_O");
+  if (v && v[0] == '0') return false;
+  const int P = 16384 / hd;
+  return (e->max_seq + P - 1) / P <= 8;
+}
+
 static wst_status_t step_eager(wse_engine *e, Marks &mk) {
   const wse_model &m = *e->m;
   const wse_config_t &c = m.c;
@@ -457,6 +469,7 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
   const float eps = c.eps;
   const float scale = (float)(1.0 / sqrt((double)hd));
   const bool fused = e->mode == WSE_STEP_FUSED;
+  const bool mio = merge_in_o(e);
 
   TRY(mk.mark(-1));
   TRY(embed_token(e));
@@ -468,10 +481,19 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
       TRY(wst_gemv_hier_rmsnorm(L.qkv.qw, L.qkv.si, L.qkv.sb, e->x, L.in_norm, eps, nullptr,
                                 L.qkv_bias, e->qkv, H, nqkv, 0));
       TRY(mk.mark(WSE_STAGE_QKV));
-      TRY(wst_attn_decode_fused(e->qkv, kc, vc, e->cos_tab, e->sin_tab, e->partials, e->attn, nq,
-                                nkv, hd, e->pos_dev, e->max_seq, scale, L.q_norm, L.k_norm, eps));
-      TRY(mk.mark(WSE_STAGE_ATTN));
-      TRY(wst_gemv_int4_hier_ex(L.o.qw, L.o.si, L.o.sb, e->attn, nullptr, e->x, nq * hd, H, 1));
+      if (mio) {
+        TRY(wst_attn_decode_slices(e->qkv, kc, vc, e->cos_tab, e->sin_tab, e->partials, nq, nkv,
+                                   hd, e->pos_dev, e->max_seq, scale, L.q_norm, L.k_norm, eps));
+        TRY(mk.mark(WSE_STAGE_ATTN));
+        TRY(wst_gemv_hier_attn(L.o.qw, L.o.si, L.o.sb, e->partials, e->x, nq, hd, e->pos_dev,
+                               e->max_seq, H, 1));
+      } else {
+        TRY(wst_attn_decode_fused(e->qkv, kc, vc, e->cos_tab, e->sin_tab, e->partials, e->attn,
+                                  nq, nkv, hd, e->pos_dev, e->max_seq, scale, L.q_norm, L.k_norm,
+                                  eps));
+        TRY(mk.mark(WSE_STAGE_ATTN));
+        TRY(wst_gemv_int4_hier_ex(L.o.qw, L.o.si, L.o.sb, e->attn, nullptr, e->x, nq * hd, H, 1));
+      }
       TRY(mk.mark(WSE_STAGE_O));
       TRY(wst_gemv_hier_swiglu(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->x, L.post_norm, eps,
                                e->act, H, I));
@@ -611,12 +633,25 @@ static wst_status_t stage_launch(wse_engine *e, int stage, int l, uint64_t *byte
       return wst_gemv_hier_rmsnorm(L.qkv.qw, L.qkv.si, L.qkv.sb, e->x, L.in_norm, eps, nullptr,
                                    L.qkv_bias, e->qkv, H, nqkv, 0);
     case WSE_STAGE_ATTN:
+      if (merge_in_o(e)) {  // the slices only; the partials go to the o GEMV
+        *bytes = 2 * (uint64_t)nkv * seq * (uint64_t)hd * 2 + (uint64_t)nqkv * 4;
+        return wst_attn_decode_slices(e->qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab,
+                                      e->sin_tab, e->partials, nq, nkv, hd, e->pos_dev,
+                                      e->max_seq, (float)(1.0 / sqrt((double)hd)), L.q_norm,
+                                      L.k_norm, eps);
+      }
       *bytes = 2 * (uint64_t)nkv * seq * (uint64_t)hd * 2 + (uint64_t)nqkv * 4 + (uint64_t)nq * hd * 2;
       return wst_attn_decode_fused(e->qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab,
                                    e->sin_tab, e->partials, e->attn, nq, nkv, hd, e->pos_dev,
                                    e->max_seq, (float)(1.0 / sqrt((double)hd)), L.q_norm,
                                    L.k_norm, eps);
     case WSE_STAGE_O:
+      if (merge_in_o(e)) {  // reads the live slices' partials instead of the f16 vector
+        const uint64_t P = 16384 / (uint64_t)hd, live = (seq + P - 1) / P;
+        *bytes = L.o.bytes() + (uint64_t)nq * live * (uint64_t)(hd + 2) * 4 + (uint64_t)H * 8;
+        return wst_gemv_hier_attn(L.o.qw, L.o.si, L.o.sb, e->partials, e->x, nq, hd, e->pos_dev,
+                                  e->max_seq, H, 1);
+      }
       *bytes = L.o.bytes() + (uint64_t)nq * hd * 2 + (uint64_t)H * 8;
       return wst_gemv_int4_hier_ex(L.o.qw, L.o.si, L.o.sb, e->attn, nullptr, e->x, nq * hd, H, 1);
     case WSE_STAGE_GATE_UP:

@@ -115,6 +115,71 @@ __device__ __forceinline__ float group_dot(const uint4 p, const XGroup &xg, uint
   return fmaf(db, 0.0625f, da) - xg.corr;
 }
 
+// The attention slices as a GEMV input (AM forms): x[h*hd + d] is the merge
+// of head h's per-slice partials (attention.hip's layout: numerators
+// [n_q][nsplit][hd], then (max, sum) pairs [n_q][nsplit][2]) for the
+// ceil(seq/P) slices holding cached positions, computed exactly as
+// attn_merge_kernel computes it and rounded to f16.
+#define AM_MAX_SLICES 8
+struct AttnIn {
+  const int32_t *pos;
+  int nsplit, hd, n_q, max_seq, P;
+};
+
+// Eight merged attention outputs (columns 8b .. 8b+7, one head) as f16, the
+// arithmetic of attn_merge_kernel for at most AM_MAX_SLICES slices (one
+// batch: every live slice in slice order, after the batch's maximum). Every
+// load is issued unconditionally (slice indices clamped), then dead slices
+// are replaced by select.
+__device__ __forceinline__ uint4 merge8(const AttnIn &am, const float *partials, int b) {
+  const int c0 = 8 * b, h = c0 / am.hd, d0 = c0 % am.hd;
+  const float *pacc = partials;
+  const float *pml = partials + (size_t)am.n_q * am.nsplit * am.hd;
+  const size_t row0 = (size_t)h * am.nsplit;
+  const int pos = *am.pos;
+  float ms[AM_MAX_SLICES], ls[AM_MAX_SLICES], vs[AM_MAX_SLICES][8];
+#pragma unroll
+  for (int sl = 0; sl < AM_MAX_SLICES; ++sl) {
+    const size_t r = row0 + min(sl, am.nsplit - 1);
+    const float2 mlv = *(const float2 *)(pml + r * 2);
+    ms[sl] = mlv.x;
+    ls[sl] = mlv.y;
+    const float4 v0 = *(const float4 *)(pacc + r * am.hd + d0);
+    const float4 v1 = *(const float4 *)(pacc + r * am.hd + d0 + 4);
+    vs[sl][0] = v0.x; vs[sl][1] = v0.y; vs[sl][2] = v0.z; vs[sl][3] = v0.w;
+    vs[sl][4] = v1.x; vs[sl][5] = v1.y; vs[sl][6] = v1.z; vs[sl][7] = v1.w;
+  }
+  const int seq = min(max(pos, 0) + 1, am.max_seq);
+  const int nactive = (seq + am.P - 1) / am.P;
+  float M = -INFINITY;
+#pragma unroll
+  for (int sl = 0; sl < AM_MAX_SLICES; ++sl) {
+    const bool live = sl < nactive;
+    ms[sl] = live ? ms[sl] : -INFINITY;
+    ls[sl] = live ? ls[sl] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vs[sl][e] = live ? vs[sl][e] : 0.0f;
+    M = fmaxf(M, ms[sl]);
+  }
+  float f[AM_MAX_SLICES];  // one exp per slice, shared by the eight columns
+  float den = 0.0f;         // the merge kernel's a *= 0, den *= 0 from -inf
+#pragma unroll
+  for (int sl = 0; sl < AM_MAX_SLICES; ++sl) {
+    f[sl] = (ms[sl] == -INFINITY) ? 0.0f : __expf(ms[sl] - M);
+    den = fmaf(ls[sl], f[sl], den);
+  }
+  uint16_t o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float a = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < AM_MAX_SLICES; ++sl) a = fmaf(vs[sl][e], f[sl], a);
+    o[e] = f2h(a / den);
+  }
+  return make_uint4(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16),
+                    o[4] | ((uint32_t)o[5] << 16), o[6] | ((uint32_t)o[7] << 16));
+}
+
 // Sum over a row's lanes when a row spans LPR <= 64 lanes of one wave (every
 // lane of the row gets the sum).
 template <int LPR>
@@ -152,13 +217,14 @@ __device__ __forceinline__ float slot_sum(float v) {
 // the current unit's compute; PD > 1: PD - 1 more units are always in flight).
 // RPW: rows per wave for short rows (WPR == 1): a row is 64 / RPW lanes of a
 // wave, so a wave streams RPW rows at once.
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW = 1>
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW = 1,
+          bool AM = false>
 __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     const uint4 *qw, const uint8_t *si,
     const uint32_t *__restrict__ sb, const void *xin,
     const uint16_t *norm_w, float eps, uint16_t *__restrict__ h_out,
     const uint16_t *__restrict__ bias, void *__restrict__ yout, int in_f, int nunits,
-    int accum) {
+    int accum, AttnIn am) {
   static_assert(!NORM || NT == NORM_THREADS, "the RMS reduction order assumes 512 threads");
   constexpr int NR = SWIGLU ? 2 : 1;
   static_assert(RPW == 1 || WPR == 1, "rows share a wave only when a row is one wave or less");
@@ -192,6 +258,8 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       xf[i][0] = a.x; xf[i][1] = a.y; xf[i][2] = a.z; xf[i][3] = a.w;
       xf[i][4] = c.x; xf[i][5] = c.y; xf[i][6] = c.z; xf[i][7] = c.w;
       nwv[i] = *(const uint4 *)(norm_w + (size_t)bc * 8);
+    } else if constexpr (AM) {
+      xh[i] = merge8(am, (const float *)xin, min(b, NB8 - 1));
     } else {
       xh[i] = *(const uint4 *)((const uint16_t *)xin + (size_t)min(b, NB8 - 1) * 8);
     }
@@ -468,13 +536,14 @@ static int blocks_per_cu() {
 }
 
 struct HierArgs {
-  const void *qw, *si, *sb, *x;
+  const void *qw, *si, *sb, *x;  // x: the partials for the AM form
   const void *norm_w;
   float eps;
   void *h_out;
   const void *bias;
   void *y;
   int in_f, nunits, accum;
+  AttnIn am;
 };
 
 // Units in flight per row slot. Measured on the 7B shapes: a second buffer
@@ -490,9 +559,9 @@ static int gemv_pd_override() {
   return v;
 }
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW>
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW, bool AM>
 static void launch_pd(const HierArgs &a) {
-  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW>;
+  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW, AM>;
   const size_t lds = (size_t)(a.in_f / HGROUP) * XQ_WORDS * 4;
   // Resident blocks per CU for this instance and LDS size, queried once.
   static thread_local size_t q_lds = (size_t)-1;
@@ -514,20 +583,20 @@ static void launch_pd(const HierArgs &a) {
   kern<<<grid, NT, lds, WST_STREAM>>>(
       (const uint4 *)a.qw, (const uint8_t *)a.si, (const uint32_t *)a.sb, a.x,
       (const uint16_t *)a.norm_w, a.eps, (uint16_t *)a.h_out, (const uint16_t *)a.bias, a.y,
-      a.in_f, a.nunits, a.accum);
+      a.in_f, a.nunits, a.accum, a.am);
 }
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1>
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1, bool AM = false>
 static void launch_q(const HierArgs &a) {
   int pd = gemv_pd_override();
   if (pd < 1 || pd > 4) {
     const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR * RPW);
     pd = a.nunits >= 8 * slots ? 2 : 1;
   }
-  if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW>(a);
-  else if (pd == 3) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW>(a);
-  else if (pd == 4) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW>(a);
-  else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW>(a);
+  if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM>(a);
+  else if (pd == 3) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM>(a);
+  else if (pd == 4) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW, AM>(a);
+  else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW, AM>(a);
 }
 
 static int gemv_rpw_override() {
@@ -540,7 +609,7 @@ static int gemv_rpw_override() {
 // long rows use 1024 so a CU builds its table once.
 #define GEMV_MAX_G 1280  // groups per row handled by the table kernel
 
-template <bool NORM, bool SWIGLU>
+template <bool NORM, bool SWIGLU, bool AM = false>
 static bool hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
   // Rows of at most 32 groups (in_f <= 1024, e.g. the 0.5B hidden 896) share a
@@ -552,20 +621,20 @@ static bool hier_dispatch(const HierArgs &a) {
   // tok/s), so four is the default for every shape (a row's bits must not
   // depend on the output count). WST_GEMV_RPW=1|2|8 selects the others.
   const int rpw = gemv_rpw_override();
-  if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4>(a);
-  else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2>(a);
-  else if (G <= 32 && rpw == 8) launch_q<4, 1, 1, 512, NORM, SWIGLU, 8>(a);
-  else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4>(a);
-  else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU>(a);
-  else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU>(a);
-  else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU>(a);
-  else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU>(a);
+  if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4, AM>(a);
+  else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2, AM>(a);
+  else if (G <= 32 && rpw == 8) launch_q<4, 1, 1, 512, NORM, SWIGLU, 8, AM>(a);
+  else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4, AM>(a);
+  else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU, 1, AM>(a);
+  else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU, 1, AM>(a);
+  else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU, 1, AM>(a);
+  else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU, 1, AM>(a);
   else if constexpr (NORM) {
-    if (G <= 512) launch_q<4, 2, 4, 512, NORM, SWIGLU>(a);
+    if (G <= 512) launch_q<4, 2, 4, 512, NORM, SWIGLU, 1, AM>(a);
     else return false;
   } else {
-    if (G <= 640) launch_q<5, 2, 3, 1024, NORM, SWIGLU>(a);
-    else if (G <= GEMV_MAX_G) launch_q<5, 4, 5, 1024, NORM, SWIGLU>(a);
+    if (G <= 640) launch_q<5, 2, 3, 1024, NORM, SWIGLU, 1, AM>(a);
+    else if (G <= GEMV_MAX_G) launch_q<5, 4, 5, 1024, NORM, SWIGLU, 1, AM>(a);
     else return false;
   }
   return true;
@@ -598,7 +667,7 @@ extern "C" wst_status_t wst_gemv_int4_hier_ex(const void *qw, const void *si, co
                                               int32_t in_f, int32_t out_f, int32_t accum) {
   const wst_status_t st = check_common(qw, si, sb, x, y, in_f, out_f, "wst_gemv_int4_hier");
   if (st != WST_OK) return st;
-  const HierArgs a{qw, si, sb, x, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum};
+  const HierArgs a{qw, si, sb, x, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum, {}};
   if (!hier_dispatch<false, false>(a)) {
     const int units = (out_f + 3) / 4;
     const int cap = wst_cu_count() * 16;
@@ -620,7 +689,7 @@ extern "C" wst_status_t wst_gemv_hier_rmsnorm(const void *qw, const void *si, co
   WST_REQUIRE(in_f / HGROUP <= 512, "wst_gemv_hier_rmsnorm: in_features above 16384");
   WST_REQUIRE(!(((uintptr_t)norm_w | (uintptr_t)h_out) & 15u),
               "wst_gemv_hier_rmsnorm: norm weight and h must be 16-byte aligned");
-  const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, bias, y, in_f, out_f, accum};
+  const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, bias, y, in_f, out_f, accum, {}};
   hier_dispatch<true, false>(a);
   WST_TRY_KERNEL("wst_gemv_hier_rmsnorm");
   return WST_OK;
@@ -634,9 +703,36 @@ extern "C" wst_status_t wst_gemv_hier_swiglu(const void *qw, const void *si, con
   WST_REQUIRE(in_f / HGROUP <= (norm_w ? 512 : GEMV_MAX_G),
               "wst_gemv_hier_swiglu: in_features above 16384 (40960 without the norm)");
   WST_REQUIRE(!((uintptr_t)norm_w & 15u), "wst_gemv_hier_swiglu: norm weight must be 16-byte aligned");
-  const HierArgs a{qw, si, sb, x, norm_w, eps, nullptr, nullptr, out, in_f, inter, 0};
+  const HierArgs a{qw, si, sb, x, norm_w, eps, nullptr, nullptr, out, in_f, inter, 0, {}};
   if (norm_w) hier_dispatch<true, true>(a);
   else hier_dispatch<false, true>(a);
   WST_TRY_KERNEL("wst_gemv_hier_swiglu");
+  return WST_OK;
+}
+
+// The attention slice merge fused into the GEMV that consumes it (the o
+// projection): y (+)= W merge(partials), bit-identical to attn_merge_kernel
+// followed by wst_gemv_int4_hier_ex. For caches of at most AM_MAX_SLICES
+// slices (max_seq <= 8 * 16384 / head_dim).
+extern "C" wst_status_t wst_gemv_hier_attn(const void *qw, const void *si, const void *sb,
+                                           const void *partials, void *y, int32_t n_q,
+                                           int32_t head_dim, const void *pos, int32_t max_seq,
+                                           int32_t out_f, int32_t accum) {
+  const int32_t in_f = n_q * head_dim;
+  const wst_status_t st = check_common(qw, si, sb, partials, y, in_f, out_f, "wst_gemv_hier_attn");
+  if (st != WST_OK) return st;
+  WST_REQUIRE(pos, "wst_gemv_hier_attn: null position");
+  WST_REQUIRE(head_dim == 64 || head_dim == 128, "wst_gemv_hier_attn: head_dim must be 64 or 128");
+  WST_REQUIRE(max_seq > 0, "wst_gemv_hier_attn: empty cache");
+  const int P = 16384 / head_dim;
+  const int nsplit = (max_seq + P - 1) / P;
+  WST_REQUIRE(nsplit <= AM_MAX_SLICES, "wst_gemv_hier_attn: more than 8 attention slices");
+  HierArgs a{qw, si, sb, partials, nullptr, 0.0f, nullptr, nullptr, y, in_f, out_f, accum,
+             {(const int32_t *)pos, nsplit, head_dim, n_q, max_seq, P}};
+  if (!hier_dispatch<false, false, true>(a)) {
+    snprintf(wst_err_buf, sizeof(wst_err_buf), "wst_gemv_hier_attn: in_features above 40960");
+    return WST_ERR_SHAPE;
+  }
+  WST_TRY_KERNEL("wst_gemv_hier_attn");
   return WST_OK;
 }
