@@ -21,6 +21,8 @@ The line printed carries:
 
     python bench.py [--steps 256] [--warmup 8] [--config 3|2] [--cpu-seconds 12]
 
+`--config 0` times the CPU reference path (the 0.5B shape, 16 + 32 greedy
+tokens, on the host) beside the GPU engine on the same weights.
 `--config 1` measures the GEMV alone (lm_head and 0.5B block shapes, weights
 cold past the MALL and hot) and prints a line of its own.
 `--config 4` instead measures the chunked prefill (0.5B shape with QK-norm and
@@ -65,7 +67,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=256)
     p.add_argument("--warmup", type=int, default=8)
-    p.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4))
+    p.add_argument("--config", type=int, default=3, choices=(0, 1, 2, 3, 4))
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline budget (tokens are added until it is spent)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -285,6 +287,72 @@ def prefill_bench(E, wk, n_new: int) -> None:
     print(json.dumps(line), flush=True)
 
 
+def cpu_reference_bench(E, wk) -> None:
+    """Config 0: the CPU reference path. The 0.5B shape with seeded weights
+    (packed on the device, copied to the oracle), a seeded 16-token prompt,
+    32 greedy tokens through oracle/oracle.c's precision-mirrored forward on
+    the host's OpenMP threads (dequant on the fly, f64 dot products); the
+    same prompt through the GPU engine beside it, tokens compared. The value
+    is the CPU's tok/s over prompt + generation, as the reference quotes its
+    CPU path; the GPU's figure for the same run is in `config`."""
+    from oracle import oracle as O
+    cfg = E.QWEN05B
+    n_prompt, n_new = 16, 32
+    g = E.Model(cfg, seed=WEIGHT_SEED)
+    ids = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt).astype(np.int32)
+    eng = E.Engine(g, n_prompt + n_new + 8)
+    eng.generate(ids, 4, chunked=False)  # warm-up
+    eng.reset()
+    wk.synchronize()
+    t0 = time.perf_counter()
+    gpu = [int(t) for t in eng.generate(ids, n_new, chunked=False)]
+    wk.synchronize()
+    gpu_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    o = O.Model(cfg, WEIGHT_SEED, pack=False)
+    copy_model_to_oracle(g, o, cfg)
+    st = O.State(o, n_prompt + n_new + 8, 0)
+    setup_s = time.perf_counter() - t0
+    log(f"config 0: CPU path, {n_prompt} prompt + {n_new} greedy tokens")
+    t0 = time.perf_counter()
+    nxt = None
+    for t in ids:
+        nxt, _ = st.step(int(t))
+    cpu = []
+    for _ in range(n_new):
+        cpu.append(int(nxt))
+        nxt, _ = st.step(int(nxt))
+    cpu_s = time.perf_counter() - t0
+    st.close()
+    # the faithful form of the reference's CPU forward (reference_numpy.py:
+    # every token recomputes the whole sequence, f64, no KV cache): one call
+    # at the final length, the cost of the last generated token
+    t0 = time.perf_counter()
+    full = o.forward_full(np.concatenate([ids, np.asarray(cpu, np.int32)]))
+    faithful_s = time.perf_counter() - t0
+    o.close()
+    eng.close()
+    g.close()
+    steps = n_prompt + n_new
+    line = {
+        "metric": "CPU reference path tok/s (config 0: Qwen2.5-0.5B shape, 16-token prompt, "
+                  "32 greedy tokens)",
+        "value": round(steps / cpu_s, 3), "unit": "tok/s", "n_gpus": 1,
+        "higher_is_better": True, "dtype": "f32 dequant, f64 dot products",
+        "data": "synthetic (seeded N(0,0.02) weights packed to int4-hier-g32; seeded prompt)",
+        "config": {"workload": "config 0: oracle/oracle.c mirrored forward, one token at a time "
+                               "with a KV cache, on the host; the GPU engine on the same weights",
+                   "cores": int(O.lib().orc_threads()), "cpu_seconds": round(cpu_s, 3),
+                   "setup_seconds_not_timed": round(setup_s, 2),
+                   "gpu_tok_s_same_run": round(steps / gpu_s, 1),
+                   "faithful_full_recompute_s_per_token_at_48": round(faithful_s, 3),
+                   "faithful_argmax_equals_last_cpu_token": bool(int(np.argmax(full)) == int(nxt)),
+                   "tokens_compared": n_new,
+                   "tokens_identical": int(sum(a == b for a, b in zip(cpu, gpu)))},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def gemv_bench(wk, reps: int) -> None:
     """Config 1: the int4-hier-g32 GEMV alone, y f32 = W x (x f16 N(0,1), W
     N(0,0.02) packed on the device), on the 0.5B lm_head shape and the 0.5B
@@ -364,6 +432,9 @@ def main():
                  "and --warmup non-negative")
 
     from whetstone_amd import engine as E, kernels as wk  # raises if not built
+    if a.config == 0:
+        cpu_reference_bench(E, wk)
+        return
     if a.config == 1:
         gemv_bench(wk, max(a.steps, 200))
         return
