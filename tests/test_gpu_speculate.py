@@ -161,3 +161,26 @@ def test_cross_entropy_refusals(model):
     with pytest.raises(ffi.WstError):
         e.cross_entropy(bad, 8)
     assert e.cross_entropy(toks[:5], 8) == (0.0, 0)  # no whole window
+
+
+def test_cross_entropy_matches_the_oracle():
+    """The device NLL against the CPU oracle's mirrored forward on the same
+    seeded weights (the device packer is bit-exact with the oracle's): the
+    per-position logits agree within the logit tolerance, so the summed NLL
+    agrees within a few 1e-3 per position."""
+    from oracle import oracle as O
+    cfg = dict(TINY, n_layers=2)
+    g, o = E.Model(cfg, seed=21), O.Model(cfg, 21)
+    V, W = cfg["vocab"], 8
+    toks = _prompt(9, 2 * W, V)
+    nll, n = E.Engine(g, 32).cross_entropy(toks, W)
+    want = 0.0
+    for w in range(2):
+        st = O.State(o, 32, 0)
+        for i in range(W - 1):
+            _, lg = st.step(int(toks[w * W + i]))
+            want += _host_nll(lg, int(toks[w * W + i + 1]))
+        st.close()
+    o.close()
+    assert n == 2 * (W - 1)
+    assert abs(nll - want) <= 3e-3 * n, (nll, want)
