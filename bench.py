@@ -419,7 +419,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
-              "(the path's sharding is described in DESIGN.md, not built)", file=sys.stderr)
+              "(multi-GPU sharding is designed, not built)", file=sys.stderr)
         sys.exit(2)
     if a.summarize:
         summarize(a.summarize, a.calibration, a.copy_probe or 256)

@@ -146,7 +146,7 @@ def test_synthetic_context_matches_oracle(orc, tiny):
 
 
 def test_step_bytes_match_the_survey_arithmetic():
-    """SURVEY 0.5B figures: weights 264,241,152 + norms/biases 143,104 +
+    """The 0.5B algorithmic bytes per token: weights 264,241,152 + norms/biases 143,104 +
     12,288 B per cached token."""
     g = E.Model(E.QWEN05B, seed=0)
     assert g.weight_bytes() == 264_241_152 + 143_104
