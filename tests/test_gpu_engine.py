@@ -145,9 +145,9 @@ def test_synthetic_context_matches_oracle(orc, tiny):
         assert np.max(np.abs(eng.logits() - want)) < 1e-2
 
 
-def test_step_bytes_match_the_survey_arithmetic():
-    """The 0.5B algorithmic bytes per token: weights 264,241,152 + norms/biases 143,104 +
-    12,288 B per cached token."""
+def test_step_bytes_match_the_format_arithmetic():
+    """The 0.5B algorithmic bytes per token (rows of in/2 + in/32 + 4 bytes):
+    weights 264,241,152 + norms/biases 143,104 + 12,288 B per cached token."""
     g = E.Model(E.QWEN05B, seed=0)
     assert g.weight_bytes() == 264_241_152 + 143_104
     eng = E.Engine(g, 1024)
