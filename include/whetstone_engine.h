@@ -150,10 +150,12 @@ wst_status_t wse_engine_rewind(wse_engine_t *e, int32_t pos);
  * last row's greedy pick in the token cursor. */
 wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids_host, int32_t n,
                                  int32_t chunked);
-/* Greedy generation (engine.rs:909-956): prefill, then n_new tokens, each read
- * back (4 bytes) from the device cursor. */
+/* Greedy generation (engine.rs:909-956): prefill, then up to n_new tokens,
+ * each read back (4 bytes) from the device cursor. Generation stops early when
+ * the context is full; *n_out receives how many tokens were written. */
 wst_status_t wse_engine_generate(wse_engine_t *e, const int32_t *prompt_host, int32_t n_prompt,
-                                 int32_t n_new, int32_t chunked, int32_t *out_tokens_host);
+                                 int32_t n_new, int32_t chunked, int32_t *out_tokens_host,
+                                 int32_t *n_out);
 wst_status_t wse_engine_token(wse_engine_t *e, int32_t *out);
 /* SpecConfig / SpecStats (speculate.rs:58-115). */
 typedef struct {

@@ -114,6 +114,63 @@ void orc_f16_to_f32_n(const uint16_t *src, float *dst, size_t n) {
 static inline float h2f(uint16_t h) { return orc_f16_to_f32(h); }
 static inline uint16_t f2h(float f) { return orc_f32_to_f16(f); }
 
+/* ------------------------------------------------ arithmetic variants
+ *
+ * The default oracle evaluates every sum in f64 and rounds once at the
+ * reference's narrowing points. The variants below exist to measure how much
+ * the decode logits depend on choices the reference leaves to the kernel:
+ *
+ *   acc = ORC_ACC_F32_SEQ   every reduction (GEMV dot, RMSNorm and QK-norm
+ *                           sums of squares, attention scores, softmax
+ *                           denominator and P.V numerators) is an f32 sum in
+ *                           ascending index order, as a scalar loop computes it
+ *   acc = ORC_ACC_F32_LANE  the same f32 terms summed as 64 lane-strided
+ *                           partials (term i to lane i % 64, ascending within a
+ *                           lane) reduced by a halving tree, as a wave does
+ *
+ * The two f32 variants differ only in summation order; every term and every
+ * other rounding is the same expression in both. xq = 1 rounds each group of
+ * 32 int4-GEMV activations to the 14-bit fixed point of the GPU kernel's
+ * activation table, X = rint(h * 2^(28-e)) * 2^(e-28) with e the f16 exponent
+ * field of the group's largest |h| (clamped to 1..30). */
+static int g_acc = ORC_ACC_F64;
+static int g_xq = 0;
+
+void orc_set_variant(int acc, int xq) {
+  g_acc = acc;
+  g_xq = xq;
+}
+
+static float sum_f32(const float *t, int64_t n) {
+  if (g_acc == ORC_ACC_F32_SEQ) {
+    float a = 0.0f;
+    for (int64_t i = 0; i < n; ++i) a += t[i];
+    return a;
+  }
+  float p[64];
+  for (int i = 0; i < 64; ++i) p[i] = 0.0f;
+  for (int64_t i = 0; i < n; ++i) p[i & 63] += t[i];
+  for (int w = 32; w >= 1; w >>= 1)
+    for (int i = 0; i < w; ++i) p[i] += p[i + w];
+  return p[0];
+}
+
+/* The GPU activation table's value of each f16 activation (xq = 1). */
+void orc_xq14(const uint16_t *x, int64_t n, double *out) {
+  for (int64_t g = 0; g < n; g += 32) {
+    const int64_t e_ = g + 32 < n ? g + 32 : n;
+    uint16_t mx = 0;
+    for (int64_t c = g; c < e_; ++c) {
+      const uint16_t a = x[c] & 0x7FFFu;
+      if (a > mx) mx = a;
+    }
+    int ef = mx >> 10;
+    ef = ef < 1 ? 1 : (ef > 30 ? 30 : ef);
+    const double sc = ldexp(1.0, ef - 28);
+    for (int64_t c = g; c < e_; ++c) out[c] = (double)rintf(h2f(x[c]) * (float)ldexp(1.0, 28 - ef)) * sc;
+  }
+}
+
 /* ---------------------------------------------------- fixture generator */
 
 /* splitmix64 (Steele, Lea, Flood 2014): the published finaliser. */
@@ -351,20 +408,32 @@ void orc_gemv_int4_hier(const uint32_t *qw, const uint8_t *si, const uint32_t *s
                         const uint16_t *x, const uint16_t *bias, float *y, int64_t in_f,
                         int64_t out_f, int accum) {
   double *xd = (double *)malloc((size_t)in_f * sizeof(double));
-  for (int64_t c = 0; c < in_f; ++c) xd[c] = (double)h2f(x[c]);
+  if (g_xq)
+    orc_xq14(x, in_f, xd);
+  else
+    for (int64_t c = 0; c < in_f; ++c) xd[c] = (double)h2f(x[c]);
 #pragma omp parallel
   {
     float *row = (float *)malloc((size_t)in_f * sizeof(float));
+    float *t = (float *)malloc((size_t)in_f * sizeof(float));
 #pragma omp for schedule(static)
     for (int64_t r = 0; r < out_f; ++r) {
       orc_dequantize_row(qw, si, sb, in_f, r, row);
-      double acc = 0.0;
-      for (int64_t c = 0; c < in_f; ++c) acc += (double)row[c] * xd[c];
-      if (bias) acc += (double)h2f(bias[r]);
-      const float rr = (float)acc;
+      float rr;
+      if (g_acc != ORC_ACC_F64) {
+        for (int64_t c = 0; c < in_f; ++c) t[c] = row[c] * (float)xd[c];
+        rr = sum_f32(t, in_f);
+        if (bias) rr += h2f(bias[r]);
+      } else {
+        double acc = 0.0;
+        for (int64_t c = 0; c < in_f; ++c) acc += (double)row[c] * xd[c];
+        if (bias) acc += (double)h2f(bias[r]);
+        rr = (float)acc;
+      }
       y[r] = accum ? y[r] + rr : rr;
     }
     free(row);
+    free(t);
   }
   free(xd);
 }
@@ -372,18 +441,38 @@ void orc_gemv_int4_hier(const uint32_t *qw, const uint8_t *si, const uint32_t *s
 /* gemv_int4.cu:194-229 (fp16 weights), same epilogue. */
 void orc_gemv_fp16(const uint16_t *w, const uint16_t *x, const uint16_t *bias, float *y,
                    int64_t in_f, int64_t out_f, int accum) {
-#pragma omp parallel for schedule(static)
-  for (int64_t r = 0; r < out_f; ++r) {
-    double acc = 0.0;
-    for (int64_t c = 0; c < in_f; ++c) acc += (double)h2f(w[r * in_f + c]) * (double)h2f(x[c]);
-    if (bias) acc += (double)h2f(bias[r]);
-    const float rr = (float)acc;
-    y[r] = accum ? y[r] + rr : rr;
+#pragma omp parallel
+  {
+    float *t = (float *)malloc((size_t)in_f * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t r = 0; r < out_f; ++r) {
+      float rr;
+      if (g_acc != ORC_ACC_F64) {
+        for (int64_t c = 0; c < in_f; ++c) t[c] = h2f(w[r * in_f + c]) * h2f(x[c]);
+        rr = sum_f32(t, in_f);
+        if (bias) rr += h2f(bias[r]);
+      } else {
+        double acc = 0.0;
+        for (int64_t c = 0; c < in_f; ++c) acc += (double)h2f(w[r * in_f + c]) * (double)h2f(x[c]);
+        if (bias) acc += (double)h2f(bias[r]);
+        rr = (float)acc;
+      }
+      y[r] = accum ? y[r] + rr : rr;
+    }
+    free(t);
   }
 }
 
 /* decode.cu:46-82: out = f16(x * rsqrt(mean(x^2) + eps) * w). */
 void orc_rmsnorm(const float *x, const uint16_t *w, uint16_t *out, int n, float eps) {
+  if (g_acc != ORC_ACC_F64) {
+    float *t = (float *)malloc((size_t)n * sizeof(float));
+    for (int i = 0; i < n; ++i) t[i] = x[i] * x[i];
+    const float inv = 1.0f / sqrtf(sum_f32(t, n) / (float)n + eps);
+    for (int i = 0; i < n; ++i) out[i] = f2h(x[i] * inv * h2f(w[i]));
+    free(t);
+    return;
+  }
   double ss = 0.0;
   for (int i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
   const double inv = 1.0 / sqrt(ss / (double)n + (double)eps);
@@ -406,6 +495,13 @@ void orc_rope_table(int max_seq, int head_dim, double theta, float *cos_tab, flo
 
 /* common.cuh:185-202: per-head RMS over hd entries, shared gain [hd]. */
 static void qk_norm_head(double *v, int hd, const uint16_t *g, float eps) {
+  if (g_acc != ORC_ACC_F64) {
+    float t[1024];
+    for (int i = 0; i < hd; ++i) t[i] = (float)v[i] * (float)v[i];
+    const float inv = 1.0f / sqrtf(sum_f32(t, hd) / (float)hd + eps);
+    for (int i = 0; i < hd; ++i) v[i] = (double)((float)v[i] * inv * h2f(g[i]));
+    return;
+  }
   double ss = 0.0;
   for (int i = 0; i < hd; ++i) ss += v[i] * v[i];
   const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
@@ -455,6 +551,32 @@ void orc_attn_decode(const float *q, const uint16_t *k_cache, const uint16_t *v_
   int seq = (pos < 0 ? 0 : pos) + 1;
   if (seq > max_seq) seq = max_seq;
   const int gqa = n_q / n_kv;
+  if (g_acc != ORC_ACC_F64) {
+    float *e = (float *)malloc((size_t)seq * sizeof(float));
+    float *t = (float *)malloc((size_t)(seq > hd ? seq : hd) * sizeof(float));
+    for (int h = 0; h < n_q; ++h) {
+      const int kvh = h / gqa;
+      float qs[1024];
+      for (int i = 0; i < hd; ++i) qs[i] = q[(size_t)h * hd + i] * scale;
+      float m = -INFINITY;
+      for (int p = 0; p < seq; ++p) {
+        const uint16_t *kt = k_cache + ((size_t)kvh * max_seq + p) * hd;
+        for (int i = 0; i < hd; ++i) t[i] = qs[i] * h2f(kt[i]);
+        e[p] = sum_f32(t, hd);
+        if (e[p] > m) m = e[p];
+      }
+      for (int p = 0; p < seq; ++p) e[p] = expf(e[p] - m);
+      const float den = sum_f32(e, seq);
+      for (int i = 0; i < hd; ++i) {
+        for (int p = 0; p < seq; ++p)
+          t[p] = e[p] * h2f(v_cache[((size_t)kvh * max_seq + p) * hd + i]);
+        out[(size_t)h * hd + i] = f2h(sum_f32(t, seq) / den);
+      }
+    }
+    free(e);
+    free(t);
+    return;
+  }
   double *sc = (double *)malloc((size_t)seq * sizeof(double));
   for (int h = 0; h < n_q; ++h) {
     const int kvh = h / gqa;

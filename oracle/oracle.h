@@ -48,6 +48,19 @@ void orc_dequantize_int4_hier(const uint32_t *qw, const uint8_t *si, const uint3
 void orc_dequantize_row(const uint32_t *qw, const uint8_t *si, const uint32_t *sb,
                         int64_t in_f, int64_t row, float *out);
 
+/* ------------------------------------------------ arithmetic variants */
+/* Process-wide switches for the drift study (not thread-safe; default 0, 0):
+ * acc ORC_ACC_F64 (f64 sums, rounded once), ORC_ACC_F32_SEQ (f32 sums in
+ * ascending order), ORC_ACC_F32_LANE (f32 sums as 64 lane-strided partials
+ * and a halving tree); xq = 1 rounds int4-GEMV activations to the GPU
+ * activation table's 14-bit per-group fixed point. */
+#define ORC_ACC_F64 0
+#define ORC_ACC_F32_SEQ 1
+#define ORC_ACC_F32_LANE 2
+void orc_set_variant(int acc, int xq);
+/* The activation table's value of each f16 activation (groups of 32). */
+void orc_xq14(const uint16_t *x, int64_t n, double *out);
+
 /* ------------------------------------------------------------ decode ops */
 /* y[r] = (accum ? y[r] : 0) + bias[r] + sum_c dequant[r][c] * f16(x)[c], f64 inside. */
 void orc_gemv_int4_hier(const uint32_t *qw, const uint8_t *si, const uint32_t *sb,

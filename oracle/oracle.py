@@ -96,6 +96,8 @@ def lib():
         "orc_state_fill_kv": (None, [C.c_void_p, C.c_uint64, C.c_int]),
         "orc_forward_full": (None, [C.c_void_p, _i32p, C.c_int, _f64p]),
         "orc_threads": (C.c_int, []),
+        "orc_set_variant": (None, [C.c_int, C.c_int]),
+        "orc_xq14": (None, [_u16p, C.c_int64, _f64p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -308,6 +310,35 @@ class State:
         logits = np.empty(self.model.cfg["vocab"], np.float32)
         nxt = lib().orc_step(self.h, token, logits)
         return int(nxt), logits
+
+
+ACC_F64, ACC_F32_SEQ, ACC_F32_LANE = 0, 1, 2
+
+
+class variant:
+    """Context manager for the oracle's arithmetic variants (process-wide):
+    `acc` picks how reductions are summed (ACC_F64 default, or f32 in
+    ascending order / as 64 lane partials and a tree), `xq` rounds int4-GEMV
+    activations to the GPU activation table's 14-bit per-group fixed point."""
+
+    def __init__(self, acc: int = ACC_F64, xq: bool = False):
+        self.acc, self.xq = int(acc), int(bool(xq))
+
+    def __enter__(self):
+        lib().orc_set_variant(self.acc, self.xq)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_variant(ACC_F64, 0)
+        return False
+
+
+def xq14(x_bits) -> np.ndarray:
+    """The activation table's value of each f16 activation (float64)."""
+    b = np.ascontiguousarray(x_bits, np.uint16)
+    out = np.empty(b.size, np.float64)
+    lib().orc_xq14(b, b.size, out)
+    return out
 
 
 def top2_margin(logits) -> float:

@@ -1,12 +1,23 @@
-"""Writes tests/golden/qwen05b_greedy.json with the CPU oracle.
+"""Writes the golden greedy streams under tests/golden/ with the CPU oracle.
 
-The oracle (oracle/oracle.c) regenerates the seeded 0.5B-shaped synthetic
-model on the host -- the same bytes the device generator packs -- and runs the
-precision-mirrored forward: 16 prompt tokens, then 64 greedy tokens, recording
-each step's top-2 logit margin (so a divergence on a near-tie can be told from
-a bug). No reference code is imported or run.
+The oracle (oracle/oracle.c) regenerates each seeded synthetic model on the
+host -- the same bytes the device generator packs (tests/test_gpu_fixture_fused.py
+checks the packer byte for byte) -- and runs the precision-mirrored forward,
+recording each step's top-2 logit margin so a divergence on a near-tie can be
+told from a bug. No reference code is imported or run.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [05b] [7b] [cfg4]    (default: 05b)
+
+  05b   qwen05b_greedy.json: 0.5B shape, 16 prompt tokens, 64 greedy tokens.
+  7b    qwen7b_ctx2048_greedy.json: the 7B shape of the headline benchmark,
+        KV caches filled with the synthetic context (seed 2) for positions
+        0..2047, one seeded token at position 2048, 64 greedy tokens; plus a
+        sample of the first step's logits (the top 64 and every 64th entry)
+        and the first step under the oracle's two f32 summation orders.
+        About 4 minutes to pack on 8 threads, 4 s per token.
+  cfg4  qwen05b_qk_rescore_4096.json: the chunked-prefill configuration (0.5B
+        shape, QK-norm, fp16 head rescore of the top 32), a seeded 4096-token
+        prompt, then 64 greedy tokens.
 """
 import json
 import sys
@@ -19,33 +30,104 @@ ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 from oracle import oracle as O  # noqa: E402
 
+HERE = Path(__file__).resolve().parent
 SEED = 0
 PROMPT_SEED = 1
-N_PROMPT, N_NEW = 16, 64
+KV_SEED = 2
+N_NEW = 64
 
 
-def main():
-    t0 = time.time()
-    m = O.Model(O.QWEN05B, SEED)
-    t1 = time.time()
-    prompt = np.random.default_rng(PROMPT_SEED).integers(0, O.QWEN05B["vocab"], N_PROMPT)
-    st = O.State(m, 256, 0)
-    for t in prompt:
-        nxt, lg = st.step(int(t))
+def _decode(st, nxt, lg, n):
     tokens, margins, top = [], [], []
-    for _ in range(N_NEW):
+    for _ in range(n):
         tokens.append(int(nxt))
         margins.append(O.top2_margin(lg))
         top.append(float(np.max(lg)))
         nxt, lg = st.step(nxt)
-    out = dict(config="qwen2.5-0.5b-shape", seed=SEED, prompt_seed=PROMPT_SEED,
-               prompt=[int(t) for t in prompt], tokens=tokens, margins=margins, top_logit=top,
-               oracle="mirrored", threads=O.lib().orc_threads(),
-               seconds=dict(model=round(t1 - t0, 1), decode=round(time.time() - t1, 1)))
-    path = Path(__file__).resolve().parent / "qwen05b_greedy.json"
+    return tokens, margins, top
+
+
+def _write(name, out, t0):
+    out["threads"] = O.lib().orc_threads()
+    out["seconds"] = round(time.time() - t0, 1)
+    path = HERE / name
     path.write_text(json.dumps(out, indent=1))
-    print(f"wrote {path} in {time.time() - t0:.1f}s; min margin {min(margins):.3g}")
+    print(f"wrote {path} in {time.time() - t0:.1f}s; min margin {min(out['margins']):.3g}",
+          flush=True)
+
+
+def golden_05b():
+    t0 = time.time()
+    m = O.Model(O.QWEN05B, SEED)
+    prompt = np.random.default_rng(PROMPT_SEED).integers(0, O.QWEN05B["vocab"], 16)
+    st = O.State(m, 256, 0)
+    for t in prompt:
+        nxt, lg = st.step(int(t))
+    tokens, margins, top = _decode(st, nxt, lg, N_NEW)
+    _write("qwen05b_greedy.json",
+           dict(config="qwen2.5-0.5b-shape", seed=SEED, prompt_seed=PROMPT_SEED,
+                prompt=[int(t) for t in prompt], tokens=tokens, margins=margins,
+                top_logit=top, oracle="mirrored"), t0)
+
+
+def golden_7b():
+    t0 = time.time()
+    ctx = 2048
+    cfg = O.QWEN7B
+    m = O.Model(cfg, SEED)
+    print(f"7b packed in {time.time() - t0:.0f}s", flush=True)
+    first = int(np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"]))
+
+    def state():
+        st = O.State(m, ctx + N_NEW + 8, 0)
+        st.fill_kv(KV_SEED, ctx)
+        st.pos = ctx
+        return st
+
+    drift = {}
+    for name, acc in (("f32_seq", O.ACC_F32_SEQ), ("f32_lane", O.ACC_F32_LANE)):
+        with O.variant(acc):
+            st = state()
+            drift[name] = st.step(first)[1].astype(np.float64)
+            st.close()
+    st = state()
+    nxt, lg = st.step(first)
+    lg0 = lg.copy()
+    tokens, margins, top = _decode(st, nxt, lg, N_NEW)
+    top64 = np.argsort(-lg0.astype(np.float64), kind="stable")[:64]
+    every = np.arange(0, cfg["vocab"], 64)
+    sample = np.unique(np.concatenate([top64, every]))
+    _write("qwen7b_ctx2048_greedy.json",
+           dict(config="qwen2.5-7b-shape", seed=SEED, kv_seed=KV_SEED, context=ctx,
+                first_token=first, tokens=tokens, margins=margins, top_logit=top,
+                oracle="mirrored",
+                first_step_logits=dict(index=[int(i) for i in sample],
+                                       value=[float(lg0[i]) for i in sample]),
+                first_step_order_drift=dict(
+                    f32_seq_vs_f32_lane=float(np.max(np.abs(drift["f32_seq"] - drift["f32_lane"]))),
+                    mirrored_vs_f32_seq=float(np.max(np.abs(lg0 - drift["f32_seq"]))),
+                    mirrored_vs_f32_lane=float(np.max(np.abs(lg0 - drift["f32_lane"]))))), t0)
+
+
+def golden_cfg4():
+    t0 = time.time()
+    cfg = dict(O.QWEN05B, qk_norm=1, rescore_k=32)
+    n_prompt = 4096
+    m = O.Model(cfg, SEED)
+    prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt)
+    st = O.State(m, n_prompt + N_NEW + 8, 0)
+    for i, t in enumerate(prompt):
+        nxt, lg = st.step(int(t))
+        if i % 512 == 511:
+            print(f"cfg4 prompt {i + 1}/{n_prompt} ({time.time() - t0:.0f}s)", flush=True)
+    tokens, margins, top = _decode(st, nxt, lg, N_NEW)
+    _write("qwen05b_qk_rescore_4096.json",
+           dict(config="qwen2.5-0.5b-shape, qk_norm, rescore_k=32", seed=SEED,
+                prompt_seed=PROMPT_SEED, n_prompt=n_prompt, tokens=tokens, margins=margins,
+                top_logit=top, oracle="mirrored"), t0)
 
 
 if __name__ == "__main__":
-    main()
+    which = sys.argv[1:] or ["05b"]
+    for w in which:
+        {"05b": golden_05b, "7b": golden_7b, "cfg4": golden_cfg4}[w]()

@@ -1,0 +1,95 @@
+"""GPU parity at the headline configuration (config 3): the Qwen2.5-7B shape.
+
+28 layers, hidden 3584, 28/4 heads of 128, intermediate 18944, vocab 152064,
+untied int4 head (crates/whetstone-core/src/config.rs:250-262); seeded
+N(0, 0.02) weights packed on the device; the KV caches hold the benchmark's
+synthetic context (seed 2) for positions 0..2047; decoding starts at position
+2048 with one seeded token, as bench.py does.
+
+Two references:
+  * the CPU oracle's precision-mirrored step on the device model's own bytes,
+    computed here (first-step logits, and the same step under the oracle's
+    two f32 summation orders);
+  * tests/golden/qwen7b_ctx2048_greedy.json, written by the oracle in the
+    build container: 64 greedy tokens with their top-2 margins and a sample
+    of the first step's logits.
+
+Tolerance. The north star reads 1e-2 max-abs / 1e-3 relative. At this depth
+two f32 implementations of the reference's step that differ only in the order
+of their sums already differ by more than that (tests/test_oracle_drift.py;
+the golden file records 0.011-0.015 on these weights), so the logit test
+asserts the GPU is no further from the oracle than 2x that order-only drift
+and reports whether the 1e-2 bar itself holds. The token stream is held to
+identical, except at an oracle near-tie.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from conftest import assert_streams, copy_model_to_oracle
+from whetstone_amd import engine as E
+
+pytestmark = pytest.mark.gpu
+GOLDEN = json.loads((Path(__file__).resolve().parent / "golden" /
+                     "qwen7b_ctx2048_greedy.json").read_text())
+CTX = GOLDEN["context"]
+N_NEW = len(GOLDEN["tokens"])
+
+
+@pytest.fixture(scope="module")
+def model7b():
+    g = E.Model(E.QWEN7B, seed=GOLDEN["seed"])
+    yield g
+    g.close()
+
+
+def _engine(g):
+    eng = E.Engine(g, CTX + N_NEW + 8)
+    eng.fill_kv(GOLDEN["kv_seed"], CTX)
+    assert eng.pos == CTX
+    return eng
+
+
+def test_7b_first_step_logits_against_oracle(orc, model7b):
+    eng = _engine(model7b)
+    eng.forward(GOLDEN["first_token"])
+    got = eng.logits().astype(np.float64)
+    tok = eng.token()
+    eng.close()
+    o = copy_model_to_oracle(orc, model7b, E.QWEN7B, GOLDEN["seed"])
+    lg = {}
+    for name, acc in (("mirrored", orc.ACC_F64), ("f32_seq", orc.ACC_F32_SEQ),
+                      ("f32_lane", orc.ACC_F32_LANE)):
+        with orc.variant(acc):
+            st = orc.State(o, CTX + 8, 0)
+            st.fill_kv(GOLDEN["kv_seed"], CTX)
+            st.pos = CTX
+            lg[name] = st.step(GOLDEN["first_token"])[1].astype(np.float64)
+            st.close()
+    o.close()
+    want = lg["mirrored"]
+    # the live oracle is the golden file's oracle
+    idx = np.asarray(GOLDEN["first_step_logits"]["index"])
+    np.testing.assert_array_equal(want[idx].astype(np.float32),
+                                  np.asarray(GOLDEN["first_step_logits"]["value"], np.float32))
+    gpu = float(np.max(np.abs(got - want)))
+    order = float(np.max(np.abs(lg["f32_seq"] - lg["f32_lane"])))
+    within = bool(np.allclose(got, want, rtol=1e-3, atol=1e-2))
+    print(f"7B first step: GPU vs mirrored oracle {gpu:.4f} max-abs "
+          f"(1e-2/1e-3 bar {'met' if within else 'not met'}); order-only drift {order:.4f}")
+    assert tok == orc.argmax(got)            # argmax bit-exact on the device logits
+    assert tok == orc.argmax(want) or orc.top2_margin(want) < 1e-4
+    assert gpu <= 2.0 * max(order, 1e-2), (gpu, order)
+    assert np.allclose(got, want, rtol=1e-3, atol=2.0 * max(order, 1e-2))
+
+
+def test_7b_greedy_stream_matches_golden_64_steps(model7b):
+    """The benchmark's own path: the captured step graph replayed per token."""
+    eng = _engine(model7b)
+    eng.capture_graph()
+    got = eng.generate(np.array([GOLDEN["first_token"]], np.int32), N_NEW, chunked=False)
+    eng.close()
+    n = assert_streams(got, GOLDEN["tokens"], GOLDEN["margins"])
+    print(f"7B greedy stream: {n}/{N_NEW} tokens identical to the oracle")

@@ -11,6 +11,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+from conftest import assert_streams
 from whetstone_amd import engine as E
 
 pytestmark = pytest.mark.gpu
@@ -70,17 +71,7 @@ def test_greedy_stream_matches_oracle_64_steps(orc, cfg):
         want.append(nxt)
         margins.append(orc.top2_margin(lg))
         nxt, lg = st.step(nxt)
-    _assert_streams(got, want, margins)
-
-
-def _assert_streams(got, want, margins, tie_margin=1e-4):
-    """Identical, or the first divergence sits on a near-tie of the oracle
-    (top-2 margin below tie_margin), where f32 rounding legitimately decides."""
-    got = list(map(int, got))
-    if got == list(map(int, want)):
-        return
-    k = next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
-    assert margins[k] < tie_margin, f"diverged at step {k}: {got[k]} vs {want[k]}, margin {margins[k]}"
+    assert_streams(got, want, margins)
 
 
 def test_fused_step_equals_reference_step_bit_for_bit(tiny):
@@ -117,19 +108,38 @@ def test_graph_replays_equal_eager_steps(tiny):
 
 
 def test_chunked_prefill_matches_sequential(orc, tiny):
+    """engine.rs:195-199: chunked prefill gives the same greedy output as
+    sequential prefill. Two chunks (256 + 44), then 32 greedy tokens from each
+    engine, token for token, and both against the oracle's stream."""
     g, o = tiny
-    prompt = _prompt(10, 300, TINY["vocab"])  # two chunks: 256 + 44
+    prompt = _prompt(10, 300, TINY["vocab"])
     a, b = E.Engine(g, 512), E.Engine(g, 512)
-    a.prefill(prompt, chunked=True)
-    b.prefill(prompt, chunked=False)
-    assert a.pos == b.pos == 300
-    la, lb = a.logits(), b.logits()
-    assert np.max(np.abs(la - lb)) < 1e-2
-    # continue both with the same steps; caches written by the two paths agree
-    for _ in range(4):
-        a.step()
-        b.step()
-        assert np.max(np.abs(a.logits() - b.logits())) < 1e-2
+    ta = a.generate(prompt, 32, chunked=True)
+    tb = b.generate(prompt, 32, chunked=False)
+    assert a.pos == b.pos == 300 + 31
+    st = orc.State(o, 512, 0)
+    for t in prompt:
+        nxt, lg = st.step(int(t))
+    want, margins = [], []
+    for _ in range(32):
+        want.append(nxt)
+        margins.append(orc.top2_margin(lg))
+        nxt, lg = st.step(nxt)
+    assert_streams(ta, tb, margins)
+    assert_streams(ta, want, margins)
+    assert_streams(tb, want, margins)
+    # the caches the two paths wrote give the same next logits within tolerance
+    assert np.allclose(a.logits(), b.logits(), rtol=1e-3, atol=1e-2)
+
+
+def test_generate_stops_when_the_context_is_full(tiny):
+    g, _ = tiny
+    eng = E.Engine(g, 24)
+    got = eng.generate(_prompt(11, 16, TINY["vocab"]), 20, chunked=False)
+    assert len(got) == 24 - 16 + 1   # the last token is picked at the full context
+    assert eng.pos == 24
+    with pytest.raises(Exception):
+        eng.capture_graph()          # no room for the warm-up step
 
 
 def test_synthetic_context_matches_oracle(orc, tiny):
@@ -163,4 +173,4 @@ def test_qwen05b_greedy_stream_matches_golden():
     g = E.Model(E.QWEN05B, seed=gold["seed"])
     eng = E.Engine(g, 256)
     got = eng.generate(np.array(gold["prompt"], np.int32), len(gold["tokens"]), chunked=False)
-    _assert_streams(got, gold["tokens"], gold["margins"])
+    assert_streams(got, gold["tokens"], gold["margins"])

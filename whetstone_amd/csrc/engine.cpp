@@ -575,6 +575,9 @@ wst_status_t wse_engine_forward(wse_engine_t *e, int32_t token) {
 wst_status_t wse_engine_capture_graph(wse_engine_t *e) {
   if (!e) return WST_ERR_INVALID_ARG;
   if (e->graph) return WST_OK;
+  // The warm-up step writes the KV slot at the current position: with a full
+  // context that slot holds a cached token and must not be overwritten.
+  TRY(check_room(e));
   // Warm every lazily initialised path (static scratch, cached device facts)
   // outside the capture, then rewind (engine.rs:357-393).
   const int saved = e->pos;
@@ -959,14 +962,17 @@ wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids, int32_t n, 
 }
 
 wst_status_t wse_engine_generate(wse_engine_t *e, const int32_t *prompt, int32_t n_prompt,
-                                 int32_t n_new, int32_t chunked, int32_t *out) {
-  if (!e || !prompt || n_prompt <= 0 || n_new < 0 || (n_new && !out)) return WST_ERR_INVALID_ARG;
+                                 int32_t n_new, int32_t chunked, int32_t *out, int32_t *n_out) {
+  if (!e || !prompt || n_prompt <= 0 || n_new < 0 || (n_new && !out) || !n_out)
+    return WST_ERR_INVALID_ARG;
+  *n_out = 0;
   TRY(wse_engine_prefill(e, prompt, n_prompt, chunked));
   int32_t next = 0;
   TRY(wse_engine_token(e, &next));
   note(e, next);  // Sampler::Greedy notes its pick (engine.rs:650-656)
   for (int i = 0; i < n_new; ++i) {
     out[i] = next;
+    *n_out = i + 1;
     if (i + 1 == n_new || e->pos >= e->max_seq) break;
     TRY(wse_engine_step(e));
     TRY(wse_engine_token(e, &next));

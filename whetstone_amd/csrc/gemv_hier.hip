@@ -24,8 +24,10 @@
 //   thread's own 8-column blocks while the block's first weight loads are in
 //   flight (activation loads are issued first; a wave's loads return in
 //   order). Entries are 80 bytes apart.
-// * The grid is persistent and balanced: every row slot gets the same number
-//   of rows, so no tail round runs on a fraction of the waves.
+// * The grid is persistent: as many blocks as the CUs hold resident (two per
+//   CU by default), units dealt round-robin so slot counts differ by at most
+//   one. (WST_GEMV_GRID=balanced instead sizes the grid so every slot gets the
+//   same count.)
 // * Per row: y = d * sum_g ls_g*Q_g - dmin * sum_g lm_g*S_g, reduced across the
 //   row's lanes with DPP (and LDS when a row spans waves). A row's value
 //   depends only on (in_f, the row's bytes, x): not on the grid or on which

@@ -65,7 +65,7 @@ _SIG = {
     "wse_engine_step": (I32, [P]),
     "wse_engine_capture_graph": (I32, [P]),
     "wse_engine_prefill": (I32, [P, P, I32, I32]),
-    "wse_engine_generate": (I32, [P, P, I32, I32, I32, P]),
+    "wse_engine_generate": (I32, [P, P, I32, I32, I32, P, P]),
     "wse_engine_token": (I32, [P, C.POINTER(I32)]),
     "wse_engine_set_token": (I32, [P, I32]),
     "wse_engine_logits": (I32, [P, P]),
@@ -298,9 +298,10 @@ class Engine:
     def generate(self, prompt, n_new: int, chunked: bool = True) -> np.ndarray:
         a = np.ascontiguousarray(prompt, np.int32)
         out = np.zeros(max(n_new, 1), np.int32)
+        n = C.c_int32()
         _check(lib().wse_engine_generate(self.h, a.ctypes.data, a.size, n_new, int(chunked),
-                                         out.ctypes.data))
-        return out[:n_new]
+                                         out.ctypes.data, C.byref(n)))
+        return out[:n.value]
 
     def chunk_width(self) -> int:
         w = C.c_int32()
