@@ -81,6 +81,16 @@ wst_status_t wst_attn_decode_fused(void *qkv, void *k_cache, void *v_cache,
                                    const void *pos, int32_t max_seq, float scale,
                                    const void *q_norm_w, const void *k_norm_w, float eps);
 
+/* wst_gemv_hier_rmsnorm(W, x, norm_w, eps, h_out, bias NULL, y, accum 0)
+ * followed by wst_argmax_advance(y, out_idx, out_f, pos, max_seq), in one
+ * launch: the GEMV's blocks keep the argmax key of the rows they write and
+ * the last block to finish combines them (pos NULL: no advance). The step's
+ * head when nothing (rescore) runs between the logits and the argmax. */
+wst_status_t wst_gemv_hier_rmsnorm_argmax(const void *qw, const void *si, const void *sb,
+                                          const void *x, const void *norm_w, float eps,
+                                          void *h_out, void *y, int32_t in_f, int32_t out_f,
+                                          void *out_idx, void *pos, int32_t max_seq);
+
 /* wst_argmax(logits, out_idx) followed by wst_advance_pos(pos, max_seq). */
 wst_status_t wst_argmax_advance(const void *logits, void *out_idx, int32_t n, void *pos,
                                 int32_t max_seq);
@@ -92,6 +102,11 @@ wst_status_t wst_argmax_advance(const void *logits, void *out_idx, int32_t n, vo
 wst_status_t wst_head_rescore_fused(const void *head, const void *x, void *logits,
                                     int32_t n, int32_t hidden, int32_t k, int32_t cap,
                                     void *scratch, int32_t nblocks);
+
+/* Cached positions per attention slice that wst_attn_decode and its fused
+ * forms use for a cache of max_seq positions: 16384 / head_dim (0 for an
+ * unsupported head_dim or an empty cache). */
+int32_t wst_attn_slice_positions(int32_t head_dim, int32_t max_seq);
 
 /* wst_attn_decode_fused without its merge kernel: the slices' partials are
  * left for wst_gemv_hier_attn. */

@@ -111,7 +111,20 @@ void orc_f16_to_f32_n(const uint16_t *src, float *dst, size_t n) {
   for (size_t i = 0; i < n; ++i) dst[i] = orc_f16_to_f32(src[i]);
 }
 
-static inline float h2f(uint16_t h) { return orc_f16_to_f32(h); }
+/* f16 -> f32 through a 64K-entry table of orc_f16_to_f32's own results. */
+static float g_h2f[65536];
+static int g_h2f_ready = 0;
+static void h2f_init(void) {
+  for (uint32_t i = 0; i < 65536; ++i) g_h2f[i] = orc_f16_to_f32((uint16_t)i);
+  __atomic_store_n(&g_h2f_ready, 1, __ATOMIC_RELEASE);
+}
+static inline float h2f(uint16_t h) {
+  if (__builtin_expect(!__atomic_load_n(&g_h2f_ready, __ATOMIC_ACQUIRE), 0)) {
+#pragma omp critical(orc_h2f_init)
+    if (!g_h2f_ready) h2f_init();
+  }
+  return g_h2f[h];
+}
 static inline uint16_t f2h(float f) { return orc_f32_to_f16(f); }
 
 /* ------------------------------------------------ arithmetic variants
@@ -577,32 +590,38 @@ void orc_attn_decode(const float *q, const uint16_t *k_cache, const uint16_t *v_
     free(t);
     return;
   }
-  double *sc = (double *)malloc((size_t)seq * sizeof(double));
-  for (int h = 0; h < n_q; ++h) {
-    const int kvh = h / gqa;
-    double qs[1024];
-    for (int i = 0; i < hd; ++i) qs[i] = (double)(q[(size_t)h * hd + i] * scale);
-    double m = -INFINITY;
-    for (int t = 0; t < seq; ++t) {
-      const uint16_t *kt = k_cache + ((size_t)kvh * max_seq + t) * hd;
-      double a = 0.0;
-      for (int i = 0; i < hd; ++i) a += qs[i] * (double)h2f(kt[i]);
-      sc[t] = a;
-      if (a > m) m = a;
+  /* Heads are independent: one per thread, each summing in the same order. */
+#pragma omp parallel if (seq * hd > 65536)
+  {
+    double *sc = (double *)malloc((size_t)seq * sizeof(double));
+#pragma omp for schedule(static)
+    for (int h = 0; h < n_q; ++h) {
+      const int kvh = h / gqa;
+      double qs[1024], num[1024];
+      for (int i = 0; i < hd; ++i) qs[i] = (double)(q[(size_t)h * hd + i] * scale);
+      double m = -INFINITY;
+      for (int t = 0; t < seq; ++t) {
+        const uint16_t *kt = k_cache + ((size_t)kvh * max_seq + t) * hd;
+        double a = 0.0;
+        for (int i = 0; i < hd; ++i) a += qs[i] * (double)h2f(kt[i]);
+        sc[t] = a;
+        if (a > m) m = a;
+      }
+      double den = 0.0;
+      for (int t = 0; t < seq; ++t) {
+        sc[t] = exp(sc[t] - m);
+        den += sc[t];
+      }
+      /* num[i] = sum_t sc[t] * v[t][i], t ascending for every i */
+      for (int i = 0; i < hd; ++i) num[i] = 0.0;
+      for (int t = 0; t < seq; ++t) {
+        const uint16_t *vt = v_cache + ((size_t)kvh * max_seq + t) * hd;
+        for (int i = 0; i < hd; ++i) num[i] += sc[t] * (double)h2f(vt[i]);
+      }
+      for (int i = 0; i < hd; ++i) out[(size_t)h * hd + i] = f2h((float)(num[i] / den));
     }
-    double den = 0.0;
-    for (int t = 0; t < seq; ++t) {
-      sc[t] = exp(sc[t] - m);
-      den += sc[t];
-    }
-    for (int i = 0; i < hd; ++i) {
-      double num = 0.0;
-      for (int t = 0; t < seq; ++t)
-        num += sc[t] * (double)h2f(v_cache[((size_t)kvh * max_seq + t) * hd + i]);
-      out[(size_t)h * hd + i] = f2h((float)(num / den));
-    }
+    free(sc);
   }
-  free(sc);
 }
 
 /* decode.cu:235-242: out = f16(g * sigmoid(g) * u), g = first half. */

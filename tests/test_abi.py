@@ -116,3 +116,14 @@ def test_python_binding_refuses_bad_shapes_before_the_boundary():
     from whetstone_amd.kernels import QuantLinearHier
     with pytest.raises(ffi.ShapeError):
         QuantLinearHier([0] * 12, [0] * 3, [0] * 1, 100, 1)
+
+
+def test_attention_slice_length_rule(hip):
+    """Positions per attention slice: 16384 / head_dim."""
+    f = hip.wst_attn_slice_positions
+    f.restype = C.c_int32
+    f.argtypes = [C.c_int32, C.c_int32]
+    cases = {(128, 1024): 128, (128, 2312): 128, (128, 40000): 128, (64, 776): 256,
+             (64, 40000): 256, (256, 300): 64, (256, 5000): 64, (100, 10): 0, (128, 0): 0}
+    for (hd, ms), want in cases.items():
+        assert f(hd, ms) == want, (hd, ms)

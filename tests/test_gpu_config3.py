@@ -32,10 +32,16 @@ from conftest import assert_streams, copy_model_to_oracle
 from whetstone_amd import engine as E
 
 pytestmark = pytest.mark.gpu
-GOLDEN = json.loads((Path(__file__).resolve().parent / "golden" /
-                     "qwen7b_ctx2048_greedy.json").read_text())
+_PATH = Path(__file__).resolve().parent / "golden" / "qwen7b_ctx2048_greedy.json"
+GOLDEN = json.loads(_PATH.read_text()) if _PATH.exists() else {"context": 0, "tokens": []}
 CTX = GOLDEN["context"]
 N_NEW = len(GOLDEN["tokens"])
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _have_golden():
+    if not _PATH.exists():
+        pytest.fail(f"{_PATH.name} is missing: python tests/golden/make_golden.py 7b")
 
 
 @pytest.fixture(scope="module")

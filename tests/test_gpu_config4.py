@@ -22,10 +22,16 @@ from conftest import assert_streams
 from whetstone_amd import engine as E
 
 pytestmark = pytest.mark.gpu
-GOLDEN = json.loads((Path(__file__).resolve().parent / "golden" /
-                     "qwen05b_qk_rescore_4096.json").read_text())
+_PATH = Path(__file__).resolve().parent / "golden" / "qwen05b_qk_rescore_4096.json"
+GOLDEN = json.loads(_PATH.read_text()) if _PATH.exists() else {"tokens": []}
 CFG = dict(E.QWEN05B, qk_norm=1, rescore_k=32)
 N_NEW = len(GOLDEN["tokens"])
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _have_golden():
+    if not _PATH.exists():
+        pytest.fail(f"{_PATH.name} is missing: python tests/golden/make_golden.py cfg4")
 
 
 @pytest.fixture(scope="module")

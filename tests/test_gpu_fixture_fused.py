@@ -136,7 +136,9 @@ def test_gemv_swiglu_equals_gemv_then_swiglu(orc, wk, in_f, inter, norm):
 @pytest.mark.parametrize("n_q,n_kv,hd,max_seq,pos,qkn", [(14, 2, 64, 1024, 600, False),
                                                          (28, 4, 128, 2304, 2100, False),
                                                          (14, 2, 64, 300, 0, True),
-                                                         (16, 8, 128, 700, 511, True)])
+                                                         (16, 8, 128, 700, 511, True),
+                                                         (28, 4, 128, 8192, 5000, True),
+                                                         (14, 2, 64, 4168, 4100, True)])
 def test_fused_attention_equals_rope_then_attention(orc, wk, n_q, n_kv, hd, max_seq, pos, qkn):
     rng = np.random.default_rng(pos + hd)
     qkv = (rng.standard_normal((n_q + 2 * n_kv) * hd) * 2).astype(np.float32)
@@ -237,3 +239,49 @@ def test_gemv_hier_attn_refuses_long_caches(orc, wk):
     with pytest.raises(ffi.WstError):
         ffi.call("wst_gemv_hier_attn", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, cache.partials.ptr,
                  y.ptr, 14, 64, wk.DeviceCursor(5).buf.ptr, 4096, 64, 0)
+
+
+@pytest.mark.parametrize("in_f,vocab", [(3584, 152064), (896, 151936), (256, 4096), (512, 40)])
+def test_head_argmax_equals_head_then_argmax_advance(orc, wk, in_f, vocab):
+    """wst_gemv_hier_rmsnorm_argmax against wst_gemv_hier_rmsnorm followed by
+    wst_argmax_advance: the same logits bit for bit, the same token (planted
+    ties between duplicated rows go to the lowest index), the same position."""
+    qw = wk.DeviceBuffer(vocab * in_f // 8, np.uint32)
+    si = wk.DeviceBuffer(vocab * in_f // 32, np.uint8)
+    sb = wk.DeviceBuffer(vocab, np.uint32)
+    ffi.call("wst_fixture_pack_hier", qw.ptr, si.ptr, sb.ptr, in_f, 0, vocab, 0, 81, 0.02)
+    rng = np.random.default_rng(in_f + vocab)
+    x = (rng.standard_normal(in_f) * 2).astype(np.float32)
+    nw = f16(orc, 1 + 0.02 * rng.standard_normal(in_f))
+    xd, nwd = wk.DeviceBuffer.from_array(x), dev_f16(wk, nw)
+    # find the winning row, then copy it over a lower and a higher row: a tie
+    y = wk.DeviceBuffer(vocab, np.float32)
+    ffi.call("wst_gemv_hier_rmsnorm", qw.ptr, si.ptr, sb.ptr, xd.ptr, nwd.ptr, 1e-6, None, None,
+             y.ptr, in_f, vocab, 0)
+    top = int(np.argmax(y.numpy()))
+    q, i_, b = qw.numpy(), si.numpy(), sb.numpy()
+    for dst in {max(top - 7, 0), min(top + 5, vocab - 1)} - {top}:
+        q[dst * in_f // 8:(dst + 1) * in_f // 8] = q[top * in_f // 8:(top + 1) * in_f // 8]
+        i_[dst * in_f // 32:(dst + 1) * in_f // 32] = i_[top * in_f // 32:(top + 1) * in_f // 32]
+        b[dst] = b[top]
+    qw.copy_from(q), si.copy_from(i_), sb.copy_from(b)
+    want_tok = min(max(top - 7, 0), top)
+    y1, h1 = wk.DeviceBuffer(vocab, np.float32), wk.DeviceBuffer(in_f, np.float16)
+    t1, p1 = wk.DeviceBuffer(1, np.int32), wk.DeviceCursor(100)
+    ffi.call("wst_gemv_hier_rmsnorm", qw.ptr, si.ptr, sb.ptr, xd.ptr, nwd.ptr, 1e-6, h1.ptr, None,
+             y1.ptr, in_f, vocab, 0)
+    ffi.call("wst_argmax_advance", y1.ptr, t1.ptr, vocab, p1.buf.ptr, 102)
+    for rep in range(3):  # repeated launches: the counter resets itself
+        y2, h2 = wk.DeviceBuffer(vocab, np.float32), wk.DeviceBuffer(in_f, np.float16)
+        t2, p2 = wk.DeviceBuffer(1, np.int32), wk.DeviceCursor(100 + rep)
+        ffi.call("wst_gemv_hier_rmsnorm_argmax", qw.ptr, si.ptr, sb.ptr, xd.ptr, nwd.ptr, 1e-6,
+                 h2.ptr, y2.ptr, in_f, vocab, t2.ptr, p2.buf.ptr, 102)
+        assert np.array_equal(y1.numpy().view(np.uint32), y2.numpy().view(np.uint32))
+        assert np.array_equal(h1.numpy().view(np.uint16), h2.numpy().view(np.uint16))
+        assert int(t2.numpy()[0]) == int(t1.numpy()[0]) == want_tok == orc.argmax(y2.numpy())
+        assert p2.get() == min(101 + rep, 102)
+    assert p1.get() == 101
+    t3 = wk.DeviceBuffer(1, np.int32)
+    ffi.call("wst_gemv_hier_rmsnorm_argmax", qw.ptr, si.ptr, sb.ptr, xd.ptr, nwd.ptr, 1e-6,
+             None, y2.ptr, in_f, vocab, t3.ptr, None, 0)   # no position to advance
+    assert int(t3.numpy()[0]) == want_tok

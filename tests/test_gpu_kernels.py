@@ -295,7 +295,11 @@ def test_attention_over_two_positions_matches_explicit_softmax(orc, wk):
                                                      (28, 4, 128, 4608, 4500),
                                                      (14, 2, 64, 9000, 8999),
                                                      # few live slices of many
-                                                     (28, 4, 128, 8192, 300)])
+                                                     (28, 4, 128, 8192, 300),
+                                                     # 313 slices of 128 (three merge batches)
+                                                     (28, 4, 128, 40000, 39000),
+                                                     # 256-dim heads in 32-position slices
+                                                     (4, 2, 256, 5000, 4321)])
 def test_attention_matches_oracle_on_random_caches(orc, wk, n_q, n_kv, hd, max_seq, pos):
     rng = np.random.default_rng(pos)
     kc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))

@@ -4,9 +4,10 @@
 //
 // MI355X design
 // -------------
-// * One 512-thread block per (kv head, slice of P cached positions), P*hd =
-//   16384 (P = 256 / 128 / 64 at hd 64 / 128 / 256). Every K/V row is read
-//   from memory once and used for all n_q/n_kv query heads of the group.
+// * One block per (kv head, slice of P cached positions), P*hd/32 threads, so
+//   each thread stages four positions of one 16-byte chunk; P = 16384 / hd
+//   (wst_attn_slice_len). Every K/V row is read from memory once and used for
+//   all n_q/n_kv query heads of the group.
 // * The block stages its slice in LDS with one batch of 16-byte loads (K as
 //   rows of positions, V transposed: rows of dims) and computes both products
 //   on MFMA (v_mfma_f32_16x16x32_f16, f32 accumulate):
@@ -19,11 +20,12 @@
 //   FMA formulation of the same block spent ~4 us of a 7.8 us single-slice
 //   launch on VALU; on MFMA the compute is a few hundred cycles.
 // * Each slice writes its unnormalised numerators and (max, sum) to the
-//   partials; a second kernel (one 64-thread block per head and 32 dims)
-//   merges the slices in slice order. Measured against merging in the last
-//   block of each kv head to finish: that costs a device-scope hand-off plus
-//   one CU pulling all of a kv head's partials, about 4.7 us; the separate
-//   merge about 3.
+//   partials; a second kernel (one 256-thread block per head and 32 dims)
+//   merges them: eight lanes per dim each merge every eighth slice, all loads
+//   issued with the position load, then a fixed tree over the eight. Measured
+//   against merging in the last block of each kv head to finish: that costs a
+//   device-scope hand-off plus one CU pulling all of a kv head's partials,
+//   about 4.7 us; the separate merge about 3.
 // * The grid covers max_seq; only the ceil(seq/P) slices holding cached
 //   positions do work, so a captured graph serves every position.
 // * ROPE form (wst_attn_decode_fused): each block applies QK-norm and RoPE to
@@ -38,16 +40,16 @@
 
 #include <stdlib.h>
 
-#define ATTN_THREADS 512
-#define ATTN_WAVES 8
 #define ATTN_MAX_GQA 8
-#define ATTN_TILE 16384      // P * hd: halves of K (and of V) a block stages
-#define ATTN_MERGE_BATCH 16  // slices fetched per round trip in the merge
+#define ATTN_MERGE_LANES 8   // lanes per dim in the merge (slices dealt round-robin)
+#define ATTN_MERGE_BATCH 16  // slices each lane fetches per round trip
 
-template <int HD>
+template <int HD, int P_>
 struct AttnShape {
-  static constexpr int P = ATTN_TILE / HD;  // positions per block
+  static constexpr int P = P_;              // positions per block
   static constexpr int CH = HD / 8;         // 16-byte chunks per row
+  static constexpr int T = P * HD / 32;     // threads: four positions of one chunk each
+  static constexpr int NW = T / 64;         // waves
   // Row strides in halves, padded by 16 bytes so that the 16 rows an MFMA
   // operand read touches fall in different LDS banks.
   static constexpr int KS = HD + 8;  // K tile  [P][KS]      (rows: positions)
@@ -81,8 +83,27 @@ static int attn_head_groups(int gqa) {
   return (gqa + hpz - 1) / hpz;
 }
 
+// Slices are 16384 / hd positions (128 at hd 128): measured on the 7B shape
+// at 2k context (4 kv heads), 32- and 64-position slices launch 4-2x the
+// blocks but run slower (slice kernel 6.8 us at 32 against 5.6 us at 128;
+// step 754 / 779 / 774 tok/s at 32 / 64 / 128), since every block pays the
+// same chain of dependent phases. WST_ATTN_SLICE=<positions> (32, 64, 128 or
+// 256, within 16384 / hd and at least 64 threads) overrides, for measurement.
+int wst_attn_slice_len(int hd, int max_seq) {
+  static int forced = -1;
+  if (forced < 0) {
+    const char *e = getenv("WST_ATTN_SLICE");
+    forced = e ? atoi(e) : 0;
+  }
+  const int pmax = 16384 / hd;
+  (void)max_seq;
+  if (forced == 32 || forced == 64 || forced == 128 || forced == 256)
+    if (forced <= pmax && forced * hd >= 2048) return forced;
+  return pmax;
+}
+
 static inline int attn_slices(int head_dim, int max_seq) {
-  const int p = ATTN_TILE / head_dim;
+  const int p = wst_attn_slice_len(head_dim, max_seq);
   return (max_seq + p - 1) / p;
 }
 
@@ -125,13 +146,13 @@ __device__ __forceinline__ void store_q(uint16_t *qh, uint16_t *ql, int at, floa
   ql[at] = f2h(v - h2f(h));
 }
 
-template <int HD, bool ROPE>
-__global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
+template <int HD, int P_, bool ROPE>
+__global__ __launch_bounds__(P_ * HD / 32) void attn_decode_kernel(
     const float *__restrict__ qkv, uint16_t *__restrict__ k_cache,
     uint16_t *__restrict__ v_cache, float *__restrict__ partials, int n_q, int n_kv,
     const int32_t *__restrict__ pos_dev, int max_seq, float scale, RopeArgs ra) {
-  using S = AttnShape<HD>;
-  constexpr int P = S::P, CH = S::CH;
+  using S = AttnShape<HD, P_>;
+  constexpr int P = S::P, CH = S::CH, T = S::T, NW = S::NW;
   (void)CH;
   extern __shared__ __align__(16) unsigned char lds[];
   uint16_t *ktile = (uint16_t *)(lds + S::K_OFF);
@@ -164,7 +185,7 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
   // ---- phase A: the slice's K and V requests go out first, all at once.
   // Thread t holds 16-byte chunk ch = t % CH (dims 8ch..8ch+7) of the four
   // consecutive positions 4 (t / CH) + i.
-  constexpr int LD = P * CH / ATTN_THREADS;
+  constexpr int LD = P * CH / T;
   static_assert(LD == 4, "four positions per thread");
   const int lch = tid % CH, lrow = 4 * (tid / CH);
   uint4 kr[LD], vr[LD];
@@ -186,7 +207,7 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
     const bool active = j < HALF;
     const float c = active ? ra.cos_tab[(size_t)pos * HALF + j] : 0.0f;
     const float s = active ? ra.sin_tab[(size_t)pos * HALF + j] : 0.0f;
-    for (int h = wave; h < hb + 1; h += ATTN_WAVES) {
+    for (int h = wave; h < hb + 1; h += NW) {
       const bool is_k = h == hb;
       if (is_k && !owner) continue;
       const float *src = is_k ? qkv + (size_t)(n_q + kvh) * HD : qkv + (size_t)(qh0 + h) * HD;
@@ -224,16 +245,16 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
       }
     }
   } else {
-    // At most 8 * 256 values: four unconditional (clamped) loads per thread,
-    // so they share one round trip.
-    constexpr int QL = ATTN_MAX_GQA * HD / ATTN_THREADS;
+    // At most 8 * HD values: unconditional (clamped) loads, so they share one
+    // round trip.
+    constexpr int QL = (ATTN_MAX_GQA * HD + T - 1) / T;
     const int nqv = hb * HD;
     float qv[QL];
 #pragma unroll
-    for (int i = 0; i < QL; ++i) qv[i] = qkv[(size_t)qh0 * HD + min(tid + i * ATTN_THREADS, nqv - 1)];
+    for (int i = 0; i < QL; ++i) qv[i] = qkv[(size_t)qh0 * HD + min(tid + i * T, nqv - 1)];
 #pragma unroll
     for (int i = 0; i < QL; ++i) {
-      const int e = tid + i * ATTN_THREADS;
+      const int e = tid + i * T;
       if (e < nqv) store_q(qh, ql, (e / HD) * S::QS + e % HD, qv[i] * scale);
     }
   }
@@ -267,7 +288,7 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
   }
   if constexpr (ROPE) {
     __syncthreads();  // the tile row of `pos` holds the cache's old contents
-    if (owner && wave == hb % ATTN_WAVES && lane < HD / 2) {
+    if (owner && wave == hb % NW && lane < HD / 2) {
       const int row = pos - t0;
       ktile[row * S::KS + lane] = knew;
       ktile[row * S::KS + lane + HD / 2] = knew2;
@@ -283,7 +304,7 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
   // tile, q as its f16 hi and lo parts so the products keep ~22 bits of q.
   {
     const int r16 = lane & 15, kq = (lane >> 4) * 8;
-    for (int nt = wave; nt < P / 16; nt += ATTN_WAVES) {
+    for (int nt = wave; nt < P / 16; nt += NW) {
       f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kk = 0; kk < HD; kk += 32) {
@@ -301,29 +322,33 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
 
   // ---- phase C: softmax over the slice, a wave per head; the weights go to
   // LDS as f16 hi and lo parts for the P.V MFMAs.
-  if (wave < hb) {
-    constexpr int R = P / 64;
+  for (int hh = wave; hh < hb; hh += NW) {
+    constexpr int R = (P + 63) / 64;
     float v[R];
     float m = -INFINITY;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      v[r] = sc[wave * P + lane + 64 * r];
+      const int p = lane + 64 * r;
+      v[r] = p < P ? sc[hh * P + p] : -INFINITY;
       m = fmaxf(m, v[r]);
     }
     m = wave_max(m);  // finite: every active slice holds a cached position
     float l = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+      const int p = lane + 64 * r;
       const float e = (v[r] == -INFINITY) ? 0.0f : __expf(v[r] - m);
       const uint16_t eh = f2h(e);
-      ph[wave * S::PS + lane + 64 * r] = eh;
-      pl[wave * S::PS + lane + 64 * r] = f2h(e - h2f(eh));
+      if (p < P) {
+        ph[hh * S::PS + p] = eh;
+        pl[hh * S::PS + p] = f2h(e - h2f(eh));
+      }
       l += e;
     }
     l = wave_sum(l);
     if (lane == 0) {
-      ml[wave * 2] = m;
-      ml[wave * 2 + 1] = l;
+      ml[hh * 2] = m;
+      ml[hh * 2 + 1] = l;
     }
   }
   __syncthreads();
@@ -334,7 +359,7 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
   float *pml = partials + (size_t)n_q * nsplit * HD;
   {
     const int r16 = lane & 15, kq = (lane >> 4) * 8;
-    for (int nd = wave; nd < HD / 16; nd += ATTN_WAVES) {
+    for (int nd = wave; nd < HD / 16; nd += NW) {
       const int d = nd * 16 + r16;
       f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
@@ -361,32 +386,57 @@ __global__ __launch_bounds__(ATTN_THREADS, 1) void attn_decode_kernel(
 // ---------------------------------------------------------------- slice merge
 //
 // out[h][d] = sum_s e^(m_s - M) acc_s[d] / sum_s e^(m_s - M) l_s with M the
-// largest slice maximum (attention.cu:170-193). One 64-thread block per (head,
-// 32 dims): lane (half, d) combines slices half*B .. half*B+B-1 of every run of
-// 2B (B = ATTN_MERGE_BATCH) in slice order, then the two halves are combined.
-// The first run's loads do not wait for the position: they are issued with it
-// (slice indices clamped to the partials' extent) and slices past the cached
-// ones are masked afterwards, so the merge costs one memory round trip, not two.
-__global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ partials,
-                                                        uint16_t *__restrict__ out, int n_q,
-                                                        int hd, int nsplit,
-                                                        const int32_t *__restrict__ pos_dev,
-                                                        int max_seq, int P) {
+// largest slice maximum (attention.cu:170-193). One block of 32*NL threads per
+// (head, 32 dims); lane group j = tid / 32 (of NL: 2 up to 32 slices, 8
+// beyond) merges slices j, j + NL, j + 2 NL, ... of dim d = tid % 32 in
+// ascending order, then the groups are combined by a fixed tree (j with
+// j + NL/2, then + NL/4, ...).
+// When the cache has at most 8 slices (SPREAD false), group 0 takes them all,
+// in slice order: the arithmetic of the merge inside the o GEMV (merge8 in
+// gemv_hier.hip), so both forms give the same bits.
+// A group's first ATTN_MERGE_BATCH slices are loaded together with the
+// position (slice indices clamped to the partials' extent), and slices past
+// the cached ones are replaced afterwards: up to 128 slices cost one memory
+// round trip per 16 NL slices.
+struct MergeState {
+  float M, den, a;
+};
+
+__device__ __forceinline__ void merge_combine(MergeState &x, const MergeState &y) {
+  if (y.M == -INFINITY) return;  // an empty partner adds nothing
+  const float Mn = fmaxf(x.M, y.M);
+  const float fo = (x.M == -INFINITY) ? 0.0f : __expf(x.M - Mn);
+  const float ft = __expf(y.M - Mn);
+  x.den = x.den * fo + y.den * ft;
+  x.a = x.a * fo + y.a * ft;
+  x.M = Mn;
+}
+
+template <int NL, bool SPREAD>
+__global__ __launch_bounds__(32 * NL) void attn_merge_kernel(const float *__restrict__ partials,
+                                                         uint16_t *__restrict__ out, int n_q,
+                                                         int hd, int nsplit,
+                                                         const int32_t *__restrict__ pos_dev,
+                                                         int max_seq, int P) {
   constexpr int B = ATTN_MERGE_BATCH;
-  __shared__ float hx[32][3];
-  const int h = blockIdx.x, d0 = blockIdx.y * 32, lane = threadIdx.x;
-  const int half = lane >> 5, d = d0 + (lane & 31);
+  __shared__ float hx[NL][32][3];
+  const int h = blockIdx.x, d0 = blockIdx.y * 32, tid = threadIdx.x;
+  const int j = tid >> 5, d = d0 + (tid & 31);
   const float *pacc = partials;
   const float *pml = partials + (size_t)n_q * nsplit * hd;
   const size_t row0 = (size_t)h * nsplit;
   const int pos = *pos_dev;
-  float M = -INFINITY, den = 0.0f, a = 0.0f;
-  int c = 0, nactive = 1;
-  do {
+  // SPREAD: group j owns slices j + NL*i; else group 0 owns slices i.
+  const int first = SPREAD ? j : (j == 0 ? 0 : nsplit);
+  const int stride = SPREAD ? NL : 1;
+  MergeState st{-INFINITY, 0.0f, 0.0f};
+  int nactive = 1;
+  for (int c = first; c < nsplit; c += B * stride) {
+    if (c != first && c >= nactive) break;  // nactive is known after the first batch
     float ms[B], ls[B], vs[B];
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const size_t r = row0 + min(c + half * B + i, nsplit - 1);
+      const size_t r = row0 + min(c + i * stride, nsplit - 1);
       const float2 mlv = *(const float2 *)(pml + r * 2);
       ms[i] = mlv.x;
       ls[i] = mlv.y;
@@ -398,58 +448,57 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
     // multiplied by zero, so nothing non-finite can enter.
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const bool live = c + half * B + i < nactive;
+      const bool live = c + i * stride < nactive;
       ms[i] = live ? ms[i] : -INFINITY;
       ls[i] = live ? ls[i] : 0.0f;
       vs[i] = live ? vs[i] : 0.0f;
     }
-    float Mn = M;
+    float Mn = st.M;
 #pragma unroll
     for (int i = 0; i < B; ++i) Mn = fmaxf(Mn, ms[i]);
-    if (Mn != -INFINITY) {  // else nothing live in this run for this half
-      const float fo = (M == -INFINITY) ? 0.0f : __expf(M - Mn);
-      a *= fo;
-      den *= fo;
+    if (Mn != -INFINITY) {  // else nothing live in this batch for this group
+      const float fo = (st.M == -INFINITY) ? 0.0f : __expf(st.M - Mn);
+      st.a *= fo;
+      st.den *= fo;
 #pragma unroll
       for (int i = 0; i < B; ++i) {
         const float f = (ms[i] == -INFINITY) ? 0.0f : __expf(ms[i] - Mn);
-        a = fmaf(vs[i], f, a);
-        den = fmaf(ls[i], f, den);
+        st.a = fmaf(vs[i], f, st.a);
+        st.den = fmaf(ls[i], f, st.den);
       }
-      M = Mn;
+      st.M = Mn;
     }
-    c += 2 * B;
-  } while (c < nactive);
-  if (half == 1) {
-    hx[lane & 31][0] = M;
-    hx[lane & 31][1] = den;
-    hx[lane & 31][2] = a;
   }
+  hx[j][tid & 31][0] = st.M;
+  hx[j][tid & 31][1] = st.den;
+  hx[j][tid & 31][2] = st.a;
   __syncthreads();
-  if (half == 0) {
-    const float Mt = hx[lane][0];
-    if (Mt != -INFINITY) {  // an empty second half adds nothing
-      const float Mn = fmaxf(M, Mt);
-      const float fo = (M == -INFINITY) ? 0.0f : __expf(M - Mn);
-      const float ft = __expf(Mt - Mn);
-      den = den * fo + hx[lane][1] * ft;
-      a = a * fo + hx[lane][2] * ft;
+#pragma unroll
+  for (int w = NL / 2; w >= 1; w >>= 1) {
+    if (j < w) {
+      const MergeState o{hx[j + w][tid & 31][0], hx[j + w][tid & 31][1], hx[j + w][tid & 31][2]};
+      merge_combine(st, o);
+      hx[j][tid & 31][0] = st.M;
+      hx[j][tid & 31][1] = st.den;
+      hx[j][tid & 31][2] = st.a;
     }
-    out[(size_t)h * hd + d] = f2h(a / den);
+    __syncthreads();
   }
+  if (j == 0) out[(size_t)h * hd + d] = f2h(st.a / st.den);
 }
 
-template <int HD, bool ROPE>
+template <int HD, int P, bool ROPE>
 static void attn_go(const dim3 grid, const void *qkv, void *k_cache, void *v_cache,
                     void *partials, int n_q, int n_kv, const void *pos, int max_seq, float scale,
                     const RopeArgs &ra) {
+  using S = AttnShape<HD, P>;
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute((const void *)attn_decode_kernel<HD, ROPE>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, AttnShape<HD>::LDS);
+    (void)hipFuncSetAttribute((const void *)attn_decode_kernel<HD, P, ROPE>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS);
     attr_set = true;
   }
-  attn_decode_kernel<HD, ROPE><<<grid, ATTN_THREADS, AttnShape<HD>::LDS, WST_STREAM>>>(
+  attn_decode_kernel<HD, P, ROPE><<<grid, S::T, S::LDS, WST_STREAM>>>(
       (const float *)qkv, (uint16_t *)k_cache, (uint16_t *)v_cache, (float *)partials, n_q,
       n_kv, (const int32_t *)pos, max_seq, scale, ra);
 }
@@ -459,26 +508,50 @@ template <bool ROPE>
 static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_cache,
                         void *partials, void *out, int n_q, int n_kv, const void *pos,
                         int max_seq, float scale, const RopeArgs &ra, bool merge = true) {
-  const int nsplit = attn_slices(head_dim, max_seq);
+  const int P = wst_attn_slice_len(head_dim, max_seq);
+  const int nsplit = (max_seq + P - 1) / P;
   const dim3 grid(n_kv, nsplit, attn_head_groups(n_q / n_kv));
-  switch (head_dim) {
-    case 64:
-      attn_go<64, ROPE>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv, pos, max_seq, scale, ra);
-      break;
-    case 128:
-      attn_go<128, ROPE>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv, pos, max_seq, scale,
-                         ra);
-      break;
+#define ATTN_GO(hd_, p_) attn_go<hd_, p_, ROPE>(grid, qkv, k_cache, v_cache, partials, n_q, \
+                                                n_kv, pos, max_seq, scale, ra)
+  switch (head_dim * 1000 + P) {
+    case 64 * 1000 + 32: ATTN_GO(64, 32); break;
+    case 64 * 1000 + 64: ATTN_GO(64, 64); break;
+    case 64 * 1000 + 128: ATTN_GO(64, 128); break;
+    case 64 * 1000 + 256: ATTN_GO(64, 256); break;
+    case 128 * 1000 + 32: ATTN_GO(128, 32); break;
+    case 128 * 1000 + 64: ATTN_GO(128, 64); break;
+    case 128 * 1000 + 128: ATTN_GO(128, 128); break;
     default:
-      if constexpr (!ROPE)
-        attn_go<256, false>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv, pos, max_seq, scale,
-                            ra);
+      if constexpr (!ROPE) {
+        if (P == 32) attn_go<256, 32, false>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv,
+                                             pos, max_seq, scale, ra);
+        else attn_go<256, 64, false>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv, pos,
+                                     max_seq, scale, ra);
+      }
       break;
   }
-  if (merge)
-    attn_merge_kernel<<<dim3(n_q, head_dim / 32), 64, 0, WST_STREAM>>>(
-      (const float *)partials, (uint16_t *)out, n_q, head_dim, nsplit,
-      (const int32_t *)pos, max_seq, ATTN_TILE / head_dim);
+#undef ATTN_GO
+  if (merge) {
+    const dim3 mg(n_q, head_dim / 32);
+    const float *pa = (const float *)partials;
+    const int32_t *pp = (const int32_t *)pos;
+    uint16_t *o = (uint16_t *)out;
+    if (nsplit <= 8)
+      attn_merge_kernel<2, false><<<mg, 64, 0, WST_STREAM>>>(pa, o, n_q, head_dim, nsplit, pp,
+                                                               max_seq, P);
+    else if (nsplit <= 2 * ATTN_MERGE_BATCH)
+      attn_merge_kernel<2, true><<<mg, 64, 0, WST_STREAM>>>(pa, o, n_q, head_dim, nsplit, pp,
+                                                              max_seq, P);
+    else
+      attn_merge_kernel<ATTN_MERGE_LANES, true><<<mg, 32 * ATTN_MERGE_LANES, 0, WST_STREAM>>>(
+          pa, o, n_q, head_dim, nsplit, pp, max_seq, P);
+  }
+}
+
+extern "C" int32_t wst_attn_slice_positions(int32_t head_dim, int32_t max_seq) {
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
+  if (max_seq <= 0) return 0;
+  return wst_attn_slice_len(head_dim, max_seq);
 }
 
 extern "C" int32_t wst_attn_partial_floats(int32_t n_q, int32_t head_dim, int32_t max_seq) {

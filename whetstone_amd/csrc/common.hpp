@@ -58,6 +58,10 @@ inline void wst_set_error_msg(const char *msg) {
 
 #define WST_STREAM hipStreamPerThread
 
+// Cached positions per decode-attention slice for a cache of max_seq
+// positions and head size hd (64, 128 or 256); defined in attention.hip.
+int wst_attn_slice_len(int hd, int max_seq);
+
 // --------------------------------------------------------- device facts
 
 // Compute units of the current device, cached per device ordinal: a property
@@ -76,6 +80,7 @@ enum {
   WST_SCRATCH_NLL = 3,
   WST_SCRATCH_ENGINE = 4,
   WST_SCRATCH_GEMM = 5,  // split-K partial sums of the chunk GEMMs
+  WST_SCRATCH_HEADMAX = 6,  // per-block argmax keys of the head GEMV's argmax form
   WST_SCRATCH_SLOTS = 8
 };
 

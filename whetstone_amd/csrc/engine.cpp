@@ -457,8 +457,14 @@ static bool merge_in_o(const wse_engine *e) {
   if (e->mode != WSE_STEP_FUSED || (hd != 64 && hd != 128)) return false;
   const char *v = getenv("WSE_MERGE_IN_O");
   if (v && v[0] == '0') return false;
-  const int P = 16384 / hd;
-  return (e->max_seq + P - 1) / P <= 8;
+  const int P = wst_attn_slice_positions(hd, e->max_seq);
+  return P > 0 && (e->max_seq + P - 1) / P <= 8;
+}
+
+// WSE_HEAD_ARGMAX=0 keeps the separate argmax launch after the head GEMV.
+static bool head_argmax_on() {
+  const char *v = getenv("WSE_HEAD_ARGMAX");
+  return !(v && v[0] == '0');
 }
 
 static wst_status_t step_eager(wse_engine *e, Marks &mk) {
@@ -518,7 +524,16 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
     TRY(wst_gemv_int4_hier_ex(L.down.qw, L.down.si, L.down.sb, e->act, nullptr, e->x, I, H, 1));
     TRY(mk.mark(WSE_STAGE_DOWN));
   }
-  TRY(head_logits(e, e->x, fused));
+  // The argmax rides on the head GEMV when nothing runs between the logits and
+  // the pick (no rescore) and the head is int4.
+  const bool head_ax = fused && e->rs_k == 0 && !m.head().dense() && head_argmax_on();
+  if (head_ax) {
+    const Mat &hm = m.head();
+    TRY(wst_gemv_hier_rmsnorm_argmax(hm.qw, hm.si, hm.sb, e->x, m.final_norm, eps, e->h,
+                                     e->logits, H, V, e->token, e->pos_dev, e->max_seq));
+  } else {
+    TRY(head_logits(e, e->x, fused));
+  }
   TRY(mk.mark(WSE_STAGE_HEAD));
   if (e->rs_k > 0) {
     if (fused) {
@@ -533,7 +548,9 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
     }
     TRY(mk.mark(WSE_STAGE_RESCORE));
   }
-  if (fused) {
+  if (head_ax) {
+    // done by the head's last block
+  } else if (fused) {
     TRY(wst_argmax_advance(e->logits, e->token, V, e->pos_dev, e->max_seq));
   } else {
     TRY(wst_argmax(e->logits, e->token, V));
@@ -650,7 +667,8 @@ static wst_status_t stage_launch(wse_engine *e, int stage, int l, uint64_t *byte
                                    L.k_norm, eps);
     case WSE_STAGE_O:
       if (merge_in_o(e)) {  // reads the live slices' partials instead of the f16 vector
-        const uint64_t P = 16384 / (uint64_t)hd, live = (seq + P - 1) / P;
+        const uint64_t P = (uint64_t)wst_attn_slice_positions(hd, e->max_seq);
+        const uint64_t live = (seq + P - 1) / P;
         *bytes = L.o.bytes() + (uint64_t)nq * live * (uint64_t)(hd + 2) * 4 + (uint64_t)H * 8;
         return wst_gemv_hier_attn(L.o.qw, L.o.si, L.o.sb, e->partials, e->x, nq, hd, e->pos_dev,
                                   e->max_seq, H, 1);
@@ -667,6 +685,11 @@ static wst_status_t stage_launch(wse_engine *e, int stage, int l, uint64_t *byte
                                    1);
     case WSE_STAGE_HEAD: {
       *bytes = m.head().bytes() + (uint64_t)H * 8 + (uint64_t)V * 4;
+      if (e->rs_k == 0 && !m.head().dense()) {  // the step's form, without the advance
+        const Mat &hm = m.head();
+        return wst_gemv_hier_rmsnorm_argmax(hm.qw, hm.si, hm.sb, e->x, m.final_norm, eps, e->h,
+                                            e->logits, H, V, e->token, nullptr, e->max_seq);
+      }
       return head_logits(e, e->x, true);
     }
     default:

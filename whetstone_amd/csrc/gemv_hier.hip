@@ -182,6 +182,26 @@ __device__ __forceinline__ uint4 merge8(const AttnIn &am, const float *partials,
                     o[4] | ((uint32_t)o[5] << 16), o[6] | ((uint32_t)o[7] << 16));
 }
 
+// The argmax epilogue (AX forms). Every block folds the argmax keys of the
+// rows it wrote into one of AX_GROUPS group maxima (block % AX_GROUPS) with a
+// relaxed agent-scope atomic max, then counts itself in the group; the last
+// block of a group folds the group maximum into the total and counts the
+// group; the last group's block writes the token, advances the position and
+// leaves every maximum and counter at zero for the next launch. Each atomic
+// waits for the previous one's result (the count's increment depends on it),
+// so a maximum is in place before the count that announces it; no cache
+// write-back or invalidate is needed, since only atomics touch these words.
+#define AX_GROUPS 8
+struct AxScratch {
+  unsigned long long gmax[AX_GROUPS], total;
+  unsigned int gcount[AX_GROUPS], count;
+};
+struct ArgmaxOut {
+  int32_t *out, *pos;
+  int max_seq;
+  AxScratch *sc;
+};
+
 // Sum over a row's lanes when a row spans LPR <= 64 lanes of one wave (every
 // lane of the row gets the sum).
 template <int LPR>
@@ -219,15 +239,17 @@ __device__ __forceinline__ float slot_sum(float v) {
 // the current unit's compute; PD > 1: PD - 1 more units are always in flight).
 // RPW: rows per wave for short rows (WPR == 1): a row is 64 / RPW lanes of a
 // wave, so a wave streams RPW rows at once.
+// AX: the argmax epilogue above (plain rows only).
 template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW = 1,
-          bool AM = false>
+          bool AM = false, bool AX = false>
 __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     const uint4 *qw, const uint8_t *si,
     const uint32_t *__restrict__ sb, const void *xin,
     const uint16_t *norm_w, float eps, uint16_t *__restrict__ h_out,
     const uint16_t *__restrict__ bias, void *__restrict__ yout, int in_f, int nunits,
-    int accum, AttnIn am) {
+    int accum, AttnIn am, ArgmaxOut ax) {
   static_assert(!NORM || NT == NORM_THREADS, "the RMS reduction order assumes 512 threads");
+  static_assert(!AX || !SWIGLU, "the argmax epilogue takes plain rows");
   constexpr int NR = SWIGLU ? 2 : 1;
   static_assert(RPW == 1 || WPR == 1, "rows share a wave only when a row is one wave or less");
   constexpr int NW = NT / 64;
@@ -348,6 +370,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   // do-while keeps the first unit's loads where they are issued: under a
   // `base < nunits` guard the compiler would move them past the barrier.
   int it = 0;
+  unsigned long long best = 0ull;  // AX: largest key of the rows this thread wrote
   // One unit from B; B is then refilled with the unit PD strides ahead, issued
   // after the compute and before the reductions and stores.
   auto process = [&](Buf &B) {
@@ -424,7 +447,12 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       } else {
         float v = part[0];
         if (bias) v += bv;
-        ((float *)yout)[row] = accum ? yv + v : v;
+        const float yr = accum ? yv + v : v;
+        ((float *)yout)[row] = yr;
+        if constexpr (AX) {
+          const unsigned long long key = argmax_key(yr, row);
+          best = key > best ? key : best;
+        }
       }
     }
     base += stride;
@@ -437,6 +465,47 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       if (PD > 1 && base >= nunits) break;
     }
   } while (base < nunits);
+  if constexpr (AX) {
+    __shared__ unsigned long long wbest[NW];
+    best = wave_max_u64(best);
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long b = wbest[0];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) b = wbest[w] > b ? wbest[w] : b;
+      const int g = blockIdx.x % AX_GROUPS;
+      const int ng = (int)gridDim.x < AX_GROUPS ? (int)gridDim.x : AX_GROUPS;
+      const unsigned int members = (gridDim.x - g + AX_GROUPS - 1) / AX_GROUPS;
+      const unsigned long long m0 =
+          __hip_atomic_fetch_max(&ax.sc->gmax[g], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // (m0 == ~0ull never happens: no key has every bit set) -- the branch
+      // makes the count wait for the maximum's completion
+      const unsigned int inc = m0 == ~0ull ? 2u : 1u;
+      const unsigned int c =
+          __hip_atomic_fetch_add(&ax.sc->gcount[g], inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (c + 1 == members) {
+        const unsigned long long gm =
+            __hip_atomic_exchange(&ax.sc->gmax[g], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&ax.sc->gcount[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long t0 =
+            __hip_atomic_fetch_max(&ax.sc->total, gm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned int inc2 = t0 == ~0ull ? 2u : 1u;
+        const unsigned int c2 =
+            __hip_atomic_fetch_add(&ax.sc->count, inc2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((int)c2 + 1 == ng) {
+          const unsigned long long tot =
+              __hip_atomic_exchange(&ax.sc->total, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(&ax.sc->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          *ax.out = (int32_t)(~(uint32_t)(tot & 0xFFFFFFFFull));
+          if (ax.pos) {
+            const int p = *ax.pos + 1;
+            *ax.pos = p < ax.max_seq ? p : ax.max_seq;
+          }
+        }
+      }
+    }
+  }
 }
 
 // Fallback for rows wider than GEMV_MAX_G groups: x is re-read from L2 per
@@ -558,6 +627,7 @@ struct HierArgs {
   void *y;
   int in_f, nunits, accum;
   AttnIn am;
+  ArgmaxOut ax;
 };
 
 // Units in flight per row slot. Measured on the 7B shapes: a second buffer
@@ -573,9 +643,10 @@ static int gemv_pd_override() {
   return v;
 }
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW, bool AM>
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW, bool AM,
+          bool AX>
 static void launch_pd(const HierArgs &a) {
-  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW, AM>;
+  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW, AM, AX>;
   const size_t lds = (size_t)(a.in_f / HGROUP) * XQ_WORDS * 4;
   // Resident blocks per CU for this instance and LDS size, queried once.
   static thread_local size_t q_lds = (size_t)-1;
@@ -599,20 +670,21 @@ static void launch_pd(const HierArgs &a) {
   kern<<<grid, NT, lds, WST_STREAM>>>(
       (const uint4 *)a.qw, (const uint8_t *)a.si, (const uint32_t *)a.sb, a.x,
       (const uint16_t *)a.norm_w, a.eps, (uint16_t *)a.h_out, (const uint16_t *)a.bias, a.y,
-      a.in_f, a.nunits, a.accum, a.am);
+      a.in_f, a.nunits, a.accum, a.am, a.ax);
 }
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1, bool AM = false>
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1, bool AM = false,
+          bool AX = false>
 static void launch_q(const HierArgs &a) {
   int pd = gemv_pd_override();
   if (pd < 1 || pd > 4) {
     const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR * RPW);
     pd = a.nunits >= 8 * slots ? 2 : 1;
   }
-  if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM>(a);
-  else if (pd == 3) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM>(a);
-  else if (pd == 4) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW, AM>(a);
-  else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW, AM>(a);
+  if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX>(a);
+  else if (pd == 3) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM, AX>(a);
+  else if (pd == 4) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW, AM, AX>(a);
+  else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW, AM, AX>(a);
 }
 
 static int gemv_rpw_override() {
@@ -625,7 +697,7 @@ static int gemv_rpw_override() {
 // long rows use 1024 so a CU builds its table once.
 #define GEMV_MAX_G 1280  // groups per row handled by the table kernel
 
-template <bool NORM, bool SWIGLU, bool AM = false>
+template <bool NORM, bool SWIGLU, bool AM = false, bool AX = false>
 static bool hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
   // Rows of at most 32 groups (in_f <= 1024, e.g. the 0.5B hidden 896) share a
@@ -637,20 +709,20 @@ static bool hier_dispatch(const HierArgs &a) {
   // tok/s), so four is the default for every shape (a row's bits must not
   // depend on the output count). WST_GEMV_RPW=1|2|8 selects the others.
   const int rpw = gemv_rpw_override();
-  if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4, AM>(a);
-  else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2, AM>(a);
-  else if (G <= 32 && rpw == 8) launch_q<4, 1, 1, 512, NORM, SWIGLU, 8, AM>(a);
-  else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4, AM>(a);
-  else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU, 1, AM>(a);
-  else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU, 1, AM>(a);
-  else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU, 1, AM>(a);
-  else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU, 1, AM>(a);
+  if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4, AM, AX>(a);
+  else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2, AM, AX>(a);
+  else if (G <= 32 && rpw == 8) launch_q<4, 1, 1, 512, NORM, SWIGLU, 8, AM, AX>(a);
+  else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4, AM, AX>(a);
+  else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU, 1, AM, AX>(a);
+  else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU, 1, AM, AX>(a);
+  else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU, 1, AM, AX>(a);
+  else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU, 1, AM, AX>(a);
   else if constexpr (NORM) {
-    if (G <= 512) launch_q<4, 2, 4, 512, NORM, SWIGLU, 1, AM>(a);
+    if (G <= 512) launch_q<4, 2, 4, 512, NORM, SWIGLU, 1, AM, AX>(a);
     else return false;
   } else {
-    if (G <= 640) launch_q<5, 2, 3, 1024, NORM, SWIGLU, 1, AM>(a);
-    else if (G <= GEMV_MAX_G) launch_q<5, 4, 5, 1024, NORM, SWIGLU, 1, AM>(a);
+    if (G <= 640) launch_q<5, 2, 3, 1024, NORM, SWIGLU, 1, AM, AX>(a);
+    else if (G <= GEMV_MAX_G) launch_q<5, 4, 5, 1024, NORM, SWIGLU, 1, AM, AX>(a);
     else return false;
   }
   return true;
@@ -683,7 +755,7 @@ extern "C" wst_status_t wst_gemv_int4_hier_ex(const void *qw, const void *si, co
                                               int32_t in_f, int32_t out_f, int32_t accum) {
   const wst_status_t st = check_common(qw, si, sb, x, y, in_f, out_f, "wst_gemv_int4_hier");
   if (st != WST_OK) return st;
-  const HierArgs a{qw, si, sb, x, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum, {}};
+  const HierArgs a{qw, si, sb, x, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum, {}, {}};
   if (!hier_dispatch<false, false>(a)) {
     const int units = (out_f + 3) / 4;
     const int cap = wst_cu_count() * 16;
@@ -705,7 +777,7 @@ extern "C" wst_status_t wst_gemv_hier_rmsnorm(const void *qw, const void *si, co
   WST_REQUIRE(in_f / HGROUP <= 512, "wst_gemv_hier_rmsnorm: in_features above 16384");
   WST_REQUIRE(!(((uintptr_t)norm_w | (uintptr_t)h_out) & 15u),
               "wst_gemv_hier_rmsnorm: norm weight and h must be 16-byte aligned");
-  const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, bias, y, in_f, out_f, accum, {}};
+  const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, bias, y, in_f, out_f, accum, {}, {}};
   hier_dispatch<true, false>(a);
   WST_TRY_KERNEL("wst_gemv_hier_rmsnorm");
   return WST_OK;
@@ -719,7 +791,7 @@ extern "C" wst_status_t wst_gemv_hier_swiglu(const void *qw, const void *si, con
   WST_REQUIRE(in_f / HGROUP <= (norm_w ? 512 : GEMV_MAX_G),
               "wst_gemv_hier_swiglu: in_features above 16384 (40960 without the norm)");
   WST_REQUIRE(!((uintptr_t)norm_w & 15u), "wst_gemv_hier_swiglu: norm weight must be 16-byte aligned");
-  const HierArgs a{qw, si, sb, x, norm_w, eps, nullptr, nullptr, out, in_f, inter, 0, {}};
+  const HierArgs a{qw, si, sb, x, norm_w, eps, nullptr, nullptr, out, in_f, inter, 0, {}, {}};
   if (norm_w) hier_dispatch<true, true>(a);
   else hier_dispatch<false, true>(a);
   WST_TRY_KERNEL("wst_gemv_hier_swiglu");
@@ -729,7 +801,8 @@ extern "C" wst_status_t wst_gemv_hier_swiglu(const void *qw, const void *si, con
 // The attention slice merge fused into the GEMV that consumes it (the o
 // projection): y (+)= W merge(partials), bit-identical to attn_merge_kernel
 // followed by wst_gemv_int4_hier_ex. For caches of at most AM_MAX_SLICES
-// slices (max_seq <= 8 * 16384 / head_dim).
+// slices (max_seq <= 8 * 16384 / head_dim, where the slices are 16384 /
+// head_dim positions long).
 extern "C" wst_status_t wst_gemv_hier_attn(const void *qw, const void *si, const void *sb,
                                            const void *partials, void *y, int32_t n_q,
                                            int32_t head_dim, const void *pos, int32_t max_seq,
@@ -740,15 +813,40 @@ extern "C" wst_status_t wst_gemv_hier_attn(const void *qw, const void *si, const
   WST_REQUIRE(pos, "wst_gemv_hier_attn: null position");
   WST_REQUIRE(head_dim == 64 || head_dim == 128, "wst_gemv_hier_attn: head_dim must be 64 or 128");
   WST_REQUIRE(max_seq > 0, "wst_gemv_hier_attn: empty cache");
-  const int P = 16384 / head_dim;
+  const int P = wst_attn_slice_len(head_dim, max_seq);
   const int nsplit = (max_seq + P - 1) / P;
   WST_REQUIRE(nsplit <= AM_MAX_SLICES, "wst_gemv_hier_attn: more than 8 attention slices");
   HierArgs a{qw, si, sb, partials, nullptr, 0.0f, nullptr, nullptr, y, in_f, out_f, accum,
-             {(const int32_t *)pos, nsplit, head_dim, n_q, max_seq, P}};
+             {(const int32_t *)pos, nsplit, head_dim, n_q, max_seq, P}, {}};
   if (!hier_dispatch<false, false, true>(a)) {
     snprintf(wst_err_buf, sizeof(wst_err_buf), "wst_gemv_hier_attn: in_features above 40960");
     return WST_ERR_SHAPE;
   }
   WST_TRY_KERNEL("wst_gemv_hier_attn");
+  return WST_OK;
+}
+
+// The head of the decode step with its argmax: wst_gemv_hier_rmsnorm (accum
+// 0, no bias) followed by wst_argmax_advance(y, out_idx, out_f, pos,
+// max_seq) in one launch (pos may be null: no advance).
+extern "C" wst_status_t wst_gemv_hier_rmsnorm_argmax(const void *qw, const void *si,
+                                                     const void *sb, const void *x,
+                                                     const void *norm_w, float eps, void *h_out,
+                                                     void *y, int32_t in_f, int32_t out_f,
+                                                     void *out_idx, void *pos, int32_t max_seq) {
+  const wst_status_t st =
+      check_common(qw, si, sb, x, y, in_f, out_f, "wst_gemv_hier_rmsnorm_argmax");
+  if (st != WST_OK) return st;
+  WST_REQUIRE(norm_w && out_idx, "wst_gemv_hier_rmsnorm_argmax: null pointer");
+  WST_REQUIRE(!pos || max_seq > 0, "wst_gemv_hier_rmsnorm_argmax: bad max_seq");
+  WST_REQUIRE(in_f / HGROUP <= 512, "wst_gemv_hier_rmsnorm_argmax: in_features above 16384");
+  WST_REQUIRE(!(((uintptr_t)norm_w | (uintptr_t)h_out) & 15u),
+              "wst_gemv_hier_rmsnorm_argmax: norm weight and h must be 16-byte aligned");
+  AxScratch *sc = (AxScratch *)wst_static_scratch(WST_SCRATCH_HEADMAX, sizeof(AxScratch));
+  if (!sc) return WST_ERR_OOM;
+  const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, nullptr, y, in_f, out_f, 0, {},
+                   {(int32_t *)out_idx, (int32_t *)pos, max_seq, sc}};
+  hier_dispatch<true, false, false, true>(a);
+  WST_TRY_KERNEL("wst_gemv_hier_rmsnorm_argmax");
   return WST_OK;
 }

@@ -96,6 +96,7 @@ ABI = {
     "wst_rope_cache": (I32, [P, P, P, P, P, I32, I32, I32, P, I32, P, P, F32]),
     "wst_attn_decode": (I32, [P, P, P, P, P, I32, I32, I32, P, I32, F32]),
     "wst_attn_partial_floats": (I32, [I32, I32, I32]),
+    "wst_attn_slice_positions": (I32, [I32, I32]),
     "wst_swiglu": (I32, [P, P, I32]),
     "wst_embed_fp16": (I32, [P, P, P, I32, I32]),
     "wst_graph_capture_begin": (I32, []),
@@ -132,6 +133,7 @@ ABI = {
     "wst_quantize_int4_hier": (I32, [P, P, P, P, I64, I64]),
     "wst_fixture_fill_kv": (I32, [P, P, I32, I32, I32, I32, U64, U64]),
     "wst_gemv_hier_rmsnorm": (I32, [P, P, P, P, P, F32, P, P, P, I32, I32, I32]),
+    "wst_gemv_hier_rmsnorm_argmax": (I32, [P, P, P, P, P, F32, P, P, I32, I32, P, P, I32]),
     "wst_gemv_hier_swiglu": (I32, [P, P, P, P, P, F32, P, I32, I32]),
     "wst_attn_decode_fused": (I32, [P, P, P, P, P, P, P, I32, I32, I32, P, I32, F32, P, P, F32]),
     "wst_argmax_advance": (I32, [P, P, I32, P, I32]),
