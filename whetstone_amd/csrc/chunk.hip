@@ -13,7 +13,7 @@ extern "C" int32_t wst_chunk_max_tokens(void) { return CHUNK_MAX_TOKENS; }
 // Implemented in gemm.hip (MFMA).
 wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void *sb,
                            const void *x, const void *bias, void *y, int32_t in_f, int32_t out_f,
-                           int32_t n, int32_t accum);
+                           int32_t n, int32_t accum, float *ws_ext = nullptr, size_t ws_cap = 0);
 
 extern "C" wst_status_t wst_gemm_int4_hier(const void *qw, const void *si, const void *sb,
                                            const void *x, const void *bias, void *y,

@@ -36,6 +36,8 @@
 //   kernel with the W tile copied instead of dequantised.
 #include "common.hpp"
 
+#include <mutex>
+
 #define HGROUP 32
 #define GM_BM 64
 #ifndef GM_BN
@@ -437,17 +439,29 @@ wst_status_t gemm_to_scratch(const void *w, const void *si, const void *sb, cons
 }
 }  // namespace
 
+// ws_ext: when non-null, the split partials go there (ws_cap bytes) instead
+// of the library's lazily grown scratch slot, and nothing is allocated.
 wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void *sb,
                            const void *x, const void *bias, void *y, int32_t in_f, int32_t out_f,
-                           int32_t n, int32_t accum) {
+                           int32_t n, int32_t accum, float *ws_ext, size_t ws_cap) {
   if (hier) set_lds_attr<true, false>();
   else set_lds_attr<false, false>();
   int splits, gps;
   plan_splits(in_f, out_f, n, &splits, &gps);
   float *ws = nullptr;
   if (splits > 1) {
-    ws = (float *)wst_static_scratch(WST_SCRATCH_GEMM, (size_t)splits * n * out_f * 4);
-    if (!ws) return WST_ERR_OOM;
+    const size_t need = (size_t)splits * n * out_f * 4;
+    if (ws_ext) {
+      if (need > ws_cap) {
+        snprintf(wst_err_buf, sizeof(wst_err_buf),
+                 "split-K partials need %zu bytes, above the %zu-byte static scratch", need, ws_cap);
+        return WST_ERR_SHAPE;
+      }
+      ws = ws_ext;
+    } else {
+      ws = (float *)wst_static_scratch(WST_SCRATCH_GEMM, need);
+      if (!ws) return WST_ERR_OOM;
+    }
   }
   const dim3 grid((out_f + GM_BM - 1) / GM_BM, (n + GM_BN - 1) / GM_BN, splits);
   if (hier)
@@ -552,5 +566,58 @@ extern "C" wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si,
       (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv, head_dim,
       pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
   WST_TRY_KERNEL("wst_gemm_hier_rope_chunk");
+  return WST_OK;
+}
+
+// ------------------------------------------- the no-allocation GEMM entry
+//
+// wst_gemm_int4_hier_noalloc: wst_gemm_int4_hier for callers that cannot
+// allocate (graph capture, serving loops). Its split-K partials live in this
+// file-scope device array instead of the lazily allocated scratch slot. The
+// split plan keeps the partials at most (CUs + tiles) x 16 KiB (6 MiB on 256
+// CUs), so 8 MiB covers every shape there; a larger need is refused.
+#define GM_NOALLOC_BYTES (8u << 20)
+static __device__ __align__(256) unsigned char scratch[GM_NOALLOC_BYTES];
+
+// The array's device address, looked up once per device with that device
+// current (each GPU holds its own copy). In host code `scratch` itself is only
+// a stand-in for the symbol and must never be passed to a kernel.
+static void *g_noalloc_scratch[64];
+static std::mutex g_noalloc_mu;
+
+static float *noalloc_scratch() {
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) {
+    snprintf(wst_err_buf, sizeof(wst_err_buf), "wst_gemm_int4_hier_noalloc: no current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_scratch[d]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      wst_set_error("wst_gemm_int4_hier_noalloc: hipGetSymbolAddress", e);
+      return nullptr;
+    }
+    g_noalloc_scratch[d] = p;
+  }
+  return (float *)g_noalloc_scratch[d];
+}
+
+extern "C" wst_status_t wst_gemm_int4_hier_noalloc(const void *qw, const void *si, const void *sb,
+                                                   const void *x, const void *bias, void *y,
+                                                   int32_t in_f, int32_t out_f, int32_t n,
+                                                   int32_t accum) {
+  WST_REQUIRE(qw && si && sb && x && y, "wst_gemm_int4_hier_noalloc: null pointer");
+  WST_REQUIRE(in_f > 0 && out_f > 0 && n > 0, "wst_gemm_int4_hier_noalloc: non-positive dimension");
+  WST_REQUIRE(in_f % 32 == 0, "wst_gemm_int4_hier_noalloc: in_features must be a multiple of 32");
+  WST_REQUIRE(!(((uintptr_t)qw | (uintptr_t)x) & 15u),
+              "wst_gemm_int4_hier_noalloc: qw and x must be 16-byte aligned");
+  float *ws = noalloc_scratch();
+  if (!ws) return WST_ERR_CUDA;
+  const wst_status_t st =
+      wst_gemm_mfma(true, qw, si, sb, x, bias, y, in_f, out_f, n, accum, ws, GM_NOALLOC_BYTES);
+  if (st != WST_OK) return st;
+  WST_TRY_KERNEL("wst_gemm_int4_hier_noalloc");
   return WST_OK;
 }
