@@ -158,11 +158,11 @@ wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si, const void
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): wst_gemm_int4_hier with the same arguments and the same
- * kernels, but its split-K partial sums go to a static 8 MiB device array
+ * kernels, but its split-K partial sums go to a static 24 MiB device array
  * (one per GPU, held until the process ends) instead of the library's lazily
  * allocated scratch. Nothing is allocated or freed. A shape whose partials
- * need more than 8 MiB is refused with WST_ERR_SHAPE (the split plan keeps
- * them within (CUs + output tiles) x 16 KiB, 6 MiB on 256 CUs). Every call on
+ * need more than 24 MiB is refused with WST_ERR_SHAPE (the split plan keeps
+ * them below (CUs + output tiles) x 64 KiB, under 24 MiB on 256 CUs). Every call on
  * one GPU shares that array: calls that overlap on one GPU (other threads'
  * streams) race. The partials are fully written before they are read, so no
  * state carries over between calls. */

@@ -41,9 +41,10 @@ def _case(orc, wk, in_f, out_f, n, seed, accum):
 
 
 def test_noalloc_gemm_equals_allocating_gemm_twice(orc, wk):
-    # 896 -> 896 over 256 tokens: 56 output tiles, K split over blocks
-    _case(orc, wk, 896, 896, 256, 11, accum=True)
-    # then a smaller input on the same static array
+    # the 0.5B down projection over a 256-token chunk: long rows, so the
+    # 64 x 256 tiles, 14 of them, K split 16 ways (14.7 MB of partials)
+    _case(orc, wk, 4864, 896, 256, 11, accum=True)
+    # then a smaller input on the same static array: 64 x 64 tiles, K split
     _case(orc, wk, 896, 200, 37, 12, accum=False)
 
 

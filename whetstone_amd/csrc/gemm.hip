@@ -283,6 +283,278 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
   }
 }
 
+// ------------------------------------------------------------ wide tiles
+//
+// gemm_wide_kernel: the same product on 64-row x 256-token tiles -- a whole
+// chunk's tokens -- with the 32x32x16 MFMA (v_mfma_f32_32x32x16_f16). Eight
+// waves each own 32 tokens x 64 rows (two 32 x 32 accumulator tiles).
+//
+// * The weights are dequantised once per 256 tokens. (The 64 x 64 tiles
+//   dequantise each weight four times per chunk; on the 7B shapes that VALU
+//   work alone was about 40% of their time.) A thread dequantises one packed
+//   word (8 weights) per step into the LDS W tile, as w = q * s + m in one f32
+//   fma -- q * s is exact in f32 (a 4-bit integer times an f16 times a 4-bit
+//   integer), so the single rounding equals the quantiser's two -- rounded to
+//   f16. The tile is double-buffered, one barrier per step.
+// * x goes memory -> LDS by DMA (global_load_lds_dwordx4: 16 bytes per lane
+//   land at M0 + 16 * lane), three steps in flight in an LDS ring, with no
+//   registers held for it. Each wave loads only its own 32 tokens (a
+//   coalesced 128-byte row per 8 lanes), so the ring needs no barrier. In LDS
+//   a token's 16-byte chunk c sits at slot c ^ (token % 8), so the MFMA
+//   operand reads (32 tokens, one chunk) spread over the banks.
+// * The packed weights (a dword and an index byte per thread per step) are
+//   loaded four steps ahead into a register ring.
+// * Every load of the loop is issued by inline asm with the wait counted by
+//   hand: left to itself the compiler sank each step's loads down to their
+//   first use, one step later, leaving one step in flight. Per step a thread
+//   issues 4 DMA ops and then 2 weight loads; x(st) is followed by exactly
+//   2 + 6 (GW_DX - 1) ops when step st is computed, so that vmcnt there
+//   covers x(st) and the weights of step st + 1, issued before it.
+// * K advances two groups (64 columns) per step; split-K and the epilogue
+//   (through LDS, token-major) are those of gemm_mfma_kernel. SWI: rows
+//   0..31 of a tile are gate rows a0..a0+31 and rows 32..63 the up rows
+//   inter+a0.., and the epilogue writes act = f16(silu(gate) * up).
+#define GW_BM 64
+#define GW_BN 256
+#define GW_THREADS 512
+#define GW_KG 2
+#define GW_KC (GW_KG * HGROUP)          // 64 columns per step
+#define GW_KS (GW_KC + 8)               // W tile row stride in halves
+#define GW_WT (GW_BM * GW_KS)           // halves of one W buffer
+#define GW_NKK (GW_KC / 16)             // MFMA k-steps per step
+#define GW_CS (GW_BM + 4)               // epilogue tile row stride (floats)
+#define GW_DX 3                         // x steps in flight (LDS ring)
+#define GW_DW 4                         // packed-weight steps in flight (registers)
+#define GW_XPAD 64                      // bytes between DMA blocks: t and t+8 on other banks
+#define GW_XWAVE (4 * (1024 + GW_XPAD)) // bytes of a wave's 32 tokens in one stage
+#define GW_XSTAGE (8 * GW_XWAVE)        // bytes of one x ring stage
+#define GW_LDS_X (GW_DX * GW_XSTAGE)
+#define GW_LDS_W (2 * GW_WT * 2)
+#define GW_LDS_C (GW_BN * GW_CS * 4)
+#define GW_LDS (GW_LDS_X + GW_LDS_W > GW_LDS_C ? GW_LDS_X + GW_LDS_W : GW_LDS_C)
+#define GW_VMCNT (2 + 6 * (GW_DX - 1))
+static_assert(GW_DW == GW_DX + 1, "the wait count assumes the weights lead x by one step");
+
+typedef float gm_f16v __attribute__((ext_vector_type(16)));
+
+template <bool HIER, bool SWI>
+__global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
+    const void *__restrict__ w, const uint8_t *__restrict__ si, const uint32_t *__restrict__ sb,
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ bias, float *__restrict__ y,
+    float *__restrict__ ws, int in_f, int out_f, int n, int accum, int gps) {
+#pragma clang fp contract(off)
+  static_assert(HIER, "the wide tiles take int4-hier weights");
+  extern __shared__ __align__(16) unsigned char gw_lds[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)gw_lds;  // byte address of the ring
+  uint16_t *wt = (uint16_t *)(gw_lds + GW_LDS_X);      // [2][GW_BM][GW_KS]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: M0 takes it
+  const int r0 = blockIdx.x * GW_BM, t0 = blockIdx.y * GW_BN;
+  const int G = in_f / HGROUP;
+  const int g_begin = blockIdx.z * gps, g_end = min(G, g_begin + gps);
+  const int steps = (g_end - g_begin + GW_KG - 1) / GW_KG;
+
+  // W assignment: tile row wr = tid / 8, group wg = (tid / 4) % 2 of the
+  // step, packed word ww = tid % 4 of the group (columns 8 ww .. 8 ww + 7).
+  const int wr = tid >> 3, wg = (tid >> 2) & 1, ww = tid & 3;
+  const int wrow = SWI ? (wr < 32 ? min(r0 / 2 + wr, out_f - 1)
+                                  : out_f + min(r0 / 2 + wr - 32, out_f - 1))
+                       : min(r0 + wr, out_f - 1);
+  // The row's (d, dmin), loaded with the prologue's loads (by asm, so that the
+  // compiler's own wait for it does not wait for those too).
+  uint32_t sbv;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(sbv) : "v"(sb + wrow) : "memory");
+  // Byte offsets from w / si of this thread's word and index at step 0; a
+  // step adds 32 bytes (qw) and 2 (si). The group index is clamped per step.
+  const uint32_t *wq_base = (const uint32_t *)w + (size_t)wrow * (in_f / 8) + ww;
+  const uint8_t *wi_base = si + (size_t)wrow * G;
+  float d = 0.0f, dm = 0.0f;  // set once the prologue's loads land
+
+  // x DMA: instruction i of wave `wave` covers tokens 8i .. 8i+7 of the wave's
+  // 32; lane l loads token 8i + l/8, chunk (l % 8) ^ (token % 8).
+  uint32_t xoff[4];  // byte offset of the lane's chunk at column 0
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tl = 8 * i + (lane >> 3);
+    const int tok = min(t0 + wave * 32 + tl, n - 1);
+    const int c = (lane & 7) ^ (tl & 7);
+    xoff[i] = (uint32_t)tok * (uint32_t)in_f * 2u + (uint32_t)c * 16u;
+  }
+  const uint32_t wave_x = lds0 + (uint32_t)wave * GW_XWAVE;
+
+  auto issue_x = [&](int step) {  // 4 DMA ops
+    step = min(step, steps - 1);
+    const int col = min((g_begin + step * GW_KG) * HGROUP, in_f - GW_KC);
+    const uint32_t stage = wave_x + (uint32_t)(step % GW_DX) * GW_XSTAGE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t m0 = stage + (uint32_t)i * (1024u + GW_XPAD);
+      const uint32_t off = xoff[i] + (uint32_t)col * 2u;
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :: "s"(m0), "v"(off), "s"(x) : "memory");
+    }
+  };
+  uint32_t wq[GW_DW], wi[GW_DW];
+  auto issue_w = [&](int step, uint32_t &q, uint32_t &ix) {  // 2 ops
+    step = min(step, steps - 1);
+    const int g = min(g_begin + step * GW_KG + wg, G - 1);
+    const uint32_t *qa = wq_base + (size_t)g * 4;
+    const uint8_t *ia = wi_base + g;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(q) : "v"(qa) : "memory");
+    asm volatile("global_load_ubyte %0, %1, off" : "=v"(ix) : "v"(ia) : "memory");
+  };
+  auto store_w = [&](uint32_t q, uint32_t ix, int step, int buf) {
+    const bool live = g_begin + step * GW_KG + wg < g_end;
+    const float s = live ? __fmul_rn(d, (float)(ix & 0xFu)) : 0.0f;
+    const float m = live ? __fmul_rn(-dm, (float)((ix >> 4) & 0xFu)) : 0.0f;
+    uint32_t hv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float lo = __builtin_fmaf((float)((q >> (8 * k)) & 0xFu), s, m);
+      const float hi = __builtin_fmaf((float)((q >> (8 * k + 4)) & 0xFu), s, m);
+      hv[k] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+    }
+    *(gm_u4 *)(wt + buf * GW_WT + wr * GW_KS + wg * HGROUP + 8 * ww) =
+        (gm_u4){hv[0], hv[1], hv[2], hv[3]};
+  };
+
+  gm_f16v acc[2];  // [row tile]
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[a][r] = 0.0f;
+
+  const int l32 = lane & 31, kh = lane >> 5;
+  // token l32 sits in DMA block l32 / 8, row l32 % 8
+  const uint32_t xrow0 = (uint32_t)(l32 >> 3) * (1024u + GW_XPAD) + (uint32_t)(l32 & 7) * 128u;
+  auto compute = [&](int step) {
+    const uint16_t *wb = wt + (step & 1) * GW_WT + l32 * GW_KS + 8 * kh;
+    const unsigned char *xs = gw_lds + (wave_x - lds0) + (uint32_t)(step % GW_DX) * GW_XSTAGE + xrow0;
+#pragma unroll
+    for (int k = 0; k < GW_NKK; ++k) {
+      const int c = 2 * k + kh;
+      const gm_h8 b = *(const gm_h8 *)(xs + (uint32_t)((c ^ (l32 & 7)) * 16));
+      const gm_h8 a0 = gm_lds8(wb + 16 * k);
+      const gm_h8 a1 = gm_lds8(wb + 32 * GW_KS + 16 * k);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc[1], 0, 0, 0);
+    }
+  };
+
+  // Prologue in the loop's issue pattern: W(0), W(1), then x(q) followed by
+  // W(q + 2) for q < GW_DX - 1.
+  issue_w(0, wq[0], wi[0]);
+  issue_w(1, wq[1], wi[1]);
+#pragma unroll
+  for (int q = 0; q < GW_DX - 1; ++q) {
+    issue_x(q);
+    issue_w(q + 2, wq[q + 2], wi[q + 2]);
+  }
+  // sb and W(0) are followed by 2 + 6 (GW_DX - 1) ops
+  asm volatile("s_waitcnt vmcnt(%3)" : "+v"(wq[0]), "+v"(wi[0]), "+v"(sbv) : "n"(GW_VMCNT)
+               : "memory");
+  d = h2f((uint16_t)(sbv & 0xFFFFu));
+  dm = h2f((uint16_t)(sbv >> 16));
+  store_w(wq[0], wi[0], 0, 0);
+  __syncthreads();
+
+  // One step: issue x(st + GW_DX - 1) and W(st + GW_DW) (into W(st)'s slot,
+  // stored a step ago), wait for x(st) and W(st + 1), multiply, dequantise
+  // W(st + 1).
+#define GW_STEP(U)                                                              \
+  {                                                                             \
+    const int st = st0 + (U);                                                   \
+    if (st >= steps) break;                                                     \
+    issue_x(st + GW_DX - 1);                                                    \
+    issue_w(st + GW_DW, wq[(U) % GW_DW], wi[(U) % GW_DW]);                      \
+    asm volatile("s_waitcnt vmcnt(%2)"                                          \
+                 : "+v"(wq[((U) + 1) % GW_DW]), "+v"(wi[((U) + 1) % GW_DW])     \
+                 : "n"(GW_VMCNT) : "memory");                                   \
+    compute(st);                                                                \
+    store_w(wq[((U) + 1) % GW_DW], wi[((U) + 1) % GW_DW], st + 1, (st + 1) & 1); \
+    __syncthreads();                                                            \
+  }
+  for (int st0 = 0; st0 < steps; st0 += GW_DW) {
+    GW_STEP(0)
+    GW_STEP(1)
+    GW_STEP(2)
+    GW_STEP(3)
+  }
+#undef GW_STEP
+  // Clamped look-ahead DMAs may still be landing in the ring, which the
+  // epilogue tile overlaps.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // Epilogue through LDS, token-major: accumulator r of row tile a holds row
+  // 32 a + 8 (r / 4) + 4 (lane / 32) + r % 4, token lane % 32 of the wave.
+  float *ct = (float *)gw_lds;  // [GW_BN][GW_CS]
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = a * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
+      ct[(wave * 32 + l32) * GW_CS + row] = acc[a][r];
+    }
+  __syncthreads();
+  if constexpr (SWI) {
+    uint16_t *act = (uint16_t *)y;
+    const int a0 = r0 / 2;
+#pragma unroll
+    for (int j = 0; j < GW_BN * 32 / 4 / GW_THREADS; ++j) {
+      const int idx = tid + GW_THREADS * j;
+      const int tl = idx / 8, kl = (idx % 8) * 4;
+      const int tok = t0 + tl;
+      if (tok >= n) continue;
+      uint16_t hv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float g = ct[tl * GW_CS + kl + e], u = ct[tl * GW_CS + 32 + kl + e];
+        hv[e] = f2h(g / (1.0f + __expf(-g)) * u);
+      }
+      uint16_t *dst = act + (size_t)tok * out_f + a0 + kl;
+      if ((out_f & 3) == 0 && a0 + kl + 3 < out_f) {
+        *(uint2 *)dst = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (a0 + kl + e < out_f) dst[e] = hv[e];
+      }
+    }
+    return;
+  }
+  const bool split = gridDim.z > 1 || ws;
+  float *dst0 = split ? ws + (size_t)blockIdx.z * n * out_f : y;
+  const bool vec = (out_f & 3) == 0;
+#pragma unroll 4
+  for (int j = 0; j < GW_BM * GW_BN / 4 / GW_THREADS; ++j) {
+    const int idx = tid + GW_THREADS * j;
+    const int tl = idx / (GW_BM / 4), rl = (idx % (GW_BM / 4)) * 4;
+    const int tok = t0 + tl, row = r0 + rl;
+    if (tok >= n || row >= out_f) continue;
+    float v[4];
+    const float4 cv = *(const float4 *)(ct + tl * GW_CS + rl);
+    v[0] = cv.x; v[1] = cv.y; v[2] = cv.z; v[3] = cv.w;
+    float *dst = dst0 + (size_t)tok * out_f + row;
+    if (!split) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (bias && row + e < out_f) v[e] += h2f(bias[row + e]);
+    }
+    if (vec) {
+      if (!split && accum) {
+        const float4 o = *(const float4 *)dst;
+        v[0] = o.x + v[0]; v[1] = o.y + v[1]; v[2] = o.z + v[2]; v[3] = o.w + v[3];
+      }
+      *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (row + e < out_f) dst[e] = (!split && accum) ? dst[e] + v[e] : v[e];
+    }
+  }
+}
+
 // sum over the splits of element i (stride `total`), in split order: the
 // loads are issued together (up to GM_MAXSPLIT), the adds stay in order.
 #define GM_MAXSPLIT 16
@@ -392,49 +664,97 @@ __global__ __launch_bounds__(64) void gemm_reduce_rope_kernel(
 }
 
 namespace {
+// The tile family: the 128 x 128 wide tiles (32x32x16 MFMA) unless
+// WST_GEMM_TILES=narrow selects the 64 x 64 tiles (16x16x32 MFMA). One choice
+// for every chunk GEMM form, so fused and unfused forms sum alike.
+bool wide_tiles() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("WST_GEMM_TILES");
+    v = (e && e[0] == 'n') ? 0 : 1;
+  }
+  return v == 1;
+}
+
 template <bool HIER, bool SWI>
 void set_lds_attr() {
   static bool done = false;
   if (!done) {
     (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<HIER, SWI>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS);
+    if constexpr (HIER)
+      (void)hipFuncSetAttribute((const void *)gemm_wide_kernel<HIER, SWI>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, GW_LDS);
     done = true;
   }
 }
 
+struct GemmPlan {
+  bool wide;
+  int bm, bn, kg;
+  int splits, gps;
+  dim3 grid;
+};
+
 // Splits so that the grid covers the chip, each at least one step long.
-void plan_splits(int in_f, int out_f, int n, int *splits, int *gps) {
+// rows: the weight matrix's row count (2 * inter for the SwiGLU form), which
+// with in_f picks the tiles: the wide tiles for long rows or many of them,
+// where their deeper pipeline pays; short K with few rows (the 0.5B qkv and
+// o projections) splits K into pieces too short for it.
+GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0) {
+  GemmPlan p;
+  if (rows <= 0) rows = out_f;
+  // (The wide tiles address x with 32-bit byte offsets.)
+  p.wide = hier && wide_tiles() && in_f >= GW_KC && (in_f >= 2048 || rows >= 4096) &&
+           (size_t)n * in_f * 2 < ((size_t)1 << 31);
+  p.bm = p.wide ? GW_BM : GM_BM;
+  p.bn = p.wide ? GW_BN : GM_BN;
+  p.kg = p.wide ? GW_KG : GM_KG;
   const int G = in_f / HGROUP;
-  const int tiles = ((out_f + GM_BM - 1) / GM_BM) * ((n + GM_BN - 1) / GM_BN);
-  *splits = 1;
-  *gps = G;
+  const int tiles = ((out_f + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
+  p.splits = 1;
+  p.gps = G;
   const int target = wst_cu_count();
   if (tiles < target / 2) {
     const int want = (target + tiles - 1) / tiles;
     int g = (G + want - 1) / want;
-    g = (g + GM_KG - 1) / GM_KG * GM_KG;
+    g = (g + p.kg - 1) / p.kg * p.kg;
     if ((G + g - 1) / g > GM_MAXSPLIT) g = (G + GM_MAXSPLIT - 1) / GM_MAXSPLIT;
-    g = (g + GM_KG - 1) / GM_KG * GM_KG;
-    *gps = g;
-    *splits = (G + g - 1) / g;
+    g = (g + p.kg - 1) / p.kg * p.kg;
+    p.gps = g;
+    p.splits = (G + g - 1) / g;
   }
+  p.grid = dim3((out_f + p.bm - 1) / p.bm, (n + p.bn - 1) / p.bn, p.splits);
+  return p;
+}
+
+template <bool HIER, bool SWI>
+void launch_gemm(const GemmPlan &p, const void *w, const void *si, const void *sb, const void *x,
+                 const void *bias, void *y, float *ws, int in_f, int out_f, int n, int accum) {
+  set_lds_attr<HIER, SWI>();
+  if constexpr (HIER) {
+    if (p.wide) {
+      gemm_wide_kernel<HIER, SWI><<<p.grid, GW_THREADS, GW_LDS, WST_STREAM>>>(
+        w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
+        (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps);
+      return;
+    }
+  }
+  gemm_mfma_kernel<HIER, SWI><<<p.grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
+        w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
+        (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps);
 }
 
 // The GEMM into the split scratch (always, even with one split): the fused
 // reduce kernels read it.
 wst_status_t gemm_to_scratch(const void *w, const void *si, const void *sb, const void *x,
                              int in_f, int out_f, int n, float **ws_out, int *splits_out) {
-  set_lds_attr<true, false>();
-  int splits, gps;
-  plan_splits(in_f, out_f, n, &splits, &gps);
-  float *ws = (float *)wst_static_scratch(WST_SCRATCH_GEMM, (size_t)splits * n * out_f * 4);
+  const GemmPlan p = plan_gemm(in_f, out_f, n);
+  float *ws = (float *)wst_static_scratch(WST_SCRATCH_GEMM, (size_t)p.splits * n * out_f * 4);
   if (!ws) return WST_ERR_OOM;
-  const dim3 grid((out_f + GM_BM - 1) / GM_BM, (n + GM_BN - 1) / GM_BN, splits);
-  gemm_mfma_kernel<true, false><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
-      w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x, nullptr, nullptr, ws,
-      in_f, out_f, n, 0, gps);
+  launch_gemm<true, false>(p, w, si, sb, x, nullptr, nullptr, ws, in_f, out_f, n, 0);
   *ws_out = ws;
-  *splits_out = splits;
+  *splits_out = p.splits;
   return WST_OK;
 }
 }  // namespace
@@ -444,10 +764,8 @@ wst_status_t gemm_to_scratch(const void *w, const void *si, const void *sb, cons
 wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void *sb,
                            const void *x, const void *bias, void *y, int32_t in_f, int32_t out_f,
                            int32_t n, int32_t accum, float *ws_ext, size_t ws_cap) {
-  if (hier) set_lds_attr<true, false>();
-  else set_lds_attr<false, false>();
-  int splits, gps;
-  plan_splits(in_f, out_f, n, &splits, &gps);
+  const GemmPlan p = plan_gemm(in_f, out_f, n, hier);
+  const int splits = p.splits;
   float *ws = nullptr;
   if (splits > 1) {
     const size_t need = (size_t)splits * n * out_f * 4;
@@ -463,15 +781,10 @@ wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void 
       if (!ws) return WST_ERR_OOM;
     }
   }
-  const dim3 grid((out_f + GM_BM - 1) / GM_BM, (n + GM_BN - 1) / GM_BN, splits);
   if (hier)
-    gemm_mfma_kernel<true, false><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
-        w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
-        (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, gps);
+    launch_gemm<true, false>(p, w, si, sb, x, bias, y, ws, in_f, out_f, n, accum);
   else
-    gemm_mfma_kernel<false, false><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
-        w, nullptr, nullptr, (const uint16_t *)x, (const uint16_t *)bias, (float *)y, ws, in_f,
-        out_f, n, accum, gps);
+    launch_gemm<false, false>(p, w, nullptr, nullptr, x, bias, y, ws, in_f, out_f, n, accum);
   if (splits > 1) {
     const size_t total = (size_t)n * out_f;
     const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
@@ -504,11 +817,12 @@ extern "C" wst_status_t wst_gemm_hier_swiglu_chunk(const void *qw, const void *s
   wst_status_t st = chunk_gemm_args(qw, si, sb, x, in_f, inter, n, "wst_gemm_hier_swiglu_chunk");
   if (st != WST_OK) return st;
   WST_REQUIRE(act, "wst_gemm_hier_swiglu_chunk: null pointer");
-  set_lds_attr<true, true>();
-  const dim3 grid((inter + 31) / 32, (n + GM_BN - 1) / GM_BN, 1);
-  gemm_mfma_kernel<true, true><<<grid, GM_THREADS, GM_LDS, WST_STREAM>>>(
-      qw, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x, nullptr, (float *)act,
-      nullptr, in_f, inter, n, 0, in_f / HGROUP);
+  // Never split: a tile pairs BM/2 gate rows with the matching up rows.
+  GemmPlan p = plan_gemm(in_f, inter, n, true, 2 * inter);
+  p.splits = 1;
+  p.gps = in_f / HGROUP;
+  p.grid = dim3((inter + p.bm / 2 - 1) / (p.bm / 2), (n + p.bn - 1) / p.bn, 1);
+  launch_gemm<true, true>(p, qw, si, sb, x, nullptr, act, nullptr, in_f, inter, n, 0);
   WST_TRY_KERNEL("wst_gemm_hier_swiglu_chunk");
   return WST_OK;
 }
@@ -574,9 +888,11 @@ extern "C" wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si,
 // wst_gemm_int4_hier_noalloc: wst_gemm_int4_hier for callers that cannot
 // allocate (graph capture, serving loops). Its split-K partials live in this
 // file-scope device array instead of the lazily allocated scratch slot. The
-// split plan keeps the partials at most (CUs + tiles) x 16 KiB (6 MiB on 256
-// CUs), so 8 MiB covers every shape there; a larger need is refused.
-#define GM_NOALLOC_BYTES (8u << 20)
+// split plan splits only grids of fewer tiles than half the CUs, at most
+// ceil(CUs / tiles) ways, so the partials stay below (CUs + tiles) x (one
+// tile, at most 64 x 256 f32 = 64 KiB): under 24 MiB on 256 CUs, which this
+// array holds; a larger need is refused.
+#define GM_NOALLOC_BYTES (24u << 20)
 static __device__ __align__(256) unsigned char scratch[GM_NOALLOC_BYTES];
 
 // The array's device address, looked up once per device with that device
