@@ -72,6 +72,13 @@ def parse():
                    help="CPU baseline budget (tokens are added until it is spent)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--stage-reps", type=int, default=20)
+    p.add_argument("--max-seq", type=int, default=0,
+                   help="KV-cache capacity for configs 2 and 3 (default: the context plus the "
+                        "generated tokens plus 8); attention's grid covers the capacity")
+    p.add_argument("--floors", action="store_true",
+                   help="with --config 2 or 3: the step's launch structure replayed as a graph "
+                        "of plain streaming reads of each kernel's bytes (the floor of that "
+                        "structure), beside a graph of the same number of empty launches")
     p.add_argument("--summarize", nargs="+", metavar="DIR",
                    help="print a text summary of rocprofv3 CSV output directories "
                         "(kernel stats, or FETCH_SIZE/WRITE_SIZE counters scaled by a "
@@ -156,6 +163,16 @@ def traffic_for(config: int, stage: str, path=None):
     return None
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def copy_model_to_oracle(g, o, cfg):
     """Device packed bytes -> the oracle's (zero-initialised) host matrices."""
     from whetstone_amd import ffi
@@ -201,14 +218,30 @@ def cpu_leg(g, cfg, ctx0, first_token, gpu_tokens, gpu_logits0, budget_s, same_c
         tb.close()
     st.close()
     n = len(toks)
+    # The reference's CPU path dequantises the model once (whetstone-quant)
+    # before its numpy forward: timed here on layer 0's four matrices and the
+    # head, projected to the whole model.
+    t = time.perf_counter()
+    for name in ("L0.qkv", "L0.o", "L0.gate_up", "L0.down"):
+        O.dequantize(o.tensor(name))
+    layer_s = time.perf_counter() - t
+    t = time.perf_counter()
+    O.dequantize(o.tensor("embed" if cfg["tied"] else "lm_head"))
+    head_s = time.perf_counter() - t
     base = {
         "value": round(n / sum(times), 4),
         "unit": "tok/s",
         "cores": int(O.lib().orc_threads()),
         "kind": "port",
+        "nproc": os.cpu_count(),
+        "cpu_model": cpu_model(),
+        "dequant_s_per_layer": round(layer_s, 3),
+        "dequant_s_model_projected": round(layer_s * cfg["n_layers"] + head_s, 2),
         "sample": (f"{n} greedy tokens from a {ctx0}-token context on the same packed weights: "
                    f"oracle/oracle.c precision-mirrored forward (dequant on the fly, f64 dot "
-                   f"products), OpenMP over rows; setup {setup_s:.1f}s not timed"),
+                   f"products), OpenMP over rows; setup {setup_s:.1f}s not timed; the whole-model "
+                   f"dequantisation of the reference's CPU path projected from layer 0 and the "
+                   f"head on the same threads"),
     }
     o.close()
     if not same_context:
@@ -284,6 +317,94 @@ def prefill_bench(E, wk, n_new: int) -> None:
     }
     eng.close()
     g.close()
+    print(json.dumps(line), flush=True)
+
+
+def floors_bench(E, wk, config: int, reps: int) -> None:
+    """The floor of the decode step's launch structure: a captured graph with
+    one launch per kernel of the fused step (per layer: norm+qkv, attention
+    slices, slice merge, o, norm+gate|up+SwiGLU, down; then the head with its
+    argmax, and the embedding row), each launch replaced by the library's
+    plain streaming read (wst_stream_read) of that kernel's algorithmic bytes
+    from its own buffer (so the weights stream cold, as in the step); and a
+    graph of the same number of minimal launches (16 bytes each), which is
+    the cost of the dependent launches alone. (With a cache of at most 8
+    attention slices the o GEMV merges them, and there is no merge launch.)
+    Prints one JSON line."""
+    from whetstone_amd import ffi
+    cfg = E.QWEN7B if config == 3 else E.QWEN05B
+    H, I, hd, nq, nkv, L, V = (cfg[k] for k in ("hidden", "inter", "head_dim", "n_q", "n_kv",
+                                                 "n_layers", "vocab"))
+    ctx = 2048 + 128 if config == 3 else 512 + 128
+    row = lambda in_f: in_f // 2 + in_f // 32 + 4
+    nqkv = (nq + 2 * nkv) * hd
+    stage_bytes = {
+        "qkv": nqkv * row(H) + H * 6 + nqkv * 6,
+        "attn": 2 * nkv * ctx * hd * 2 + nqkv * 4,
+        "merge": nq * -(-ctx // (16384 // hd)) * (hd + 2) * 4 + nq * hd * 2,
+        "o": H * row(nq * hd) + nq * hd * 2 + H * 8,
+        "gate_up": 2 * I * row(H) + H * 6 + I * 2,
+        "down": H * row(I) + I * 2 + H * 8,
+    }
+    if ctx + 136 <= 8 * (16384 // hd):  # short caches: the o GEMV merges the slices itself
+        stage_bytes["o"] += stage_bytes.pop("merge") - nq * hd * 2
+    head_bytes = V * row(H) + H * 8 + V * 4
+    per_layer = [(k, -(-b // 256) * 256) for k, b in stage_bytes.items()]
+    total = sum(b for _, b in per_layer) * L + head_bytes + H * 4
+    buf = wk.DeviceBuffer(total + 4096, np.uint8)
+    ffi.call("wst_memset", buf.ptr, 1, total + 4096)
+    sink = wk.DeviceBuffer(4, np.float32)
+    base = buf.ptr.value
+    launches = []
+    off = 0
+    for _ in range(L):
+        for k, b in per_layer:
+            launches.append((off, b))
+            off += b
+    launches.append((off, -(-head_bytes // 256) * 256))
+    off += launches[-1][1]
+    launches.append((off, H * 4))  # the next step's embedding row
+    wk.synchronize()
+
+    def run(graph_fn, n_rep):
+        g = wk.Graph.capture(graph_fn)
+        for _ in range(3):
+            g.launch()
+        wk.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n_rep):
+            g.launch()
+        wk.synchronize()
+        dt = (time.perf_counter() - t0) / n_rep
+        g.close()
+        return dt
+
+    def stream_graph():
+        for o, b in launches:
+            ffi.call("wst_stream_read", base + o, b, sink.ptr)
+
+    def empty_graph():
+        for _ in launches:
+            ffi.call("wst_stream_read", base, 16, sink.ptr)
+
+    t_stream = run(stream_graph, reps)
+    t_empty = run(empty_graph, reps)
+    n = len(launches)
+    line = {
+        "metric": f"decode-step launch-structure floors (config {config})",
+        "value": round(1.0 / t_stream, 1), "unit": "tok/s", "n_gpus": 1,
+        "higher_is_better": True, "data": "synthetic (streaming reads of each kernel's bytes)",
+        "config": {"workload": f"config {config}: {n} dependent launches per token "
+                               f"({L} layers x {len(per_layer)} + head + embedding), context "
+                               f"{ctx}, as one captured graph",
+                   "bytes_per_token": total,
+                   "stream_graph_us_per_token": round(t_stream * 1e6, 1),
+                   "stream_graph_gbs": round(total / t_stream / 1e9, 1),
+                   "empty_graph_us_per_token": round(t_empty * 1e6, 1),
+                   "empty_graph_us_per_launch": round(t_empty * 1e6 / n, 3),
+                   "hbm_time_at_8tbs_us": round(total / HBM_PEAK_GBS / 1e3, 1),
+                   "launches": n, "reps": reps},
+    }
     print(json.dumps(line), flush=True)
 
 
@@ -395,6 +516,26 @@ def gemv_bench(wk, reps: int) -> None:
             us = e0.elapsed_ms(e1) * 1e3 / reps
             out[mode] = {"us_per_call": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
                          "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        if name == "lm_head":
+            # the floor: the library's streaming read of the same bytes per
+            # call, cycling through as many distinct copies (weights cold)
+            buf = wk.DeviceBuffer(copies * nbytes, np.uint8)
+            ffi.call("wst_memset", buf.ptr, 1, copies * nbytes)
+            sink = wk.DeviceBuffer(4, np.float32)
+            for k in range(10):
+                ffi.call("wst_stream_read", buf.ptr.value + (k % copies) * nbytes, nbytes, sink.ptr)
+            e0, e1 = wk.Event(), wk.Event()
+            e0.record()
+            for k in range(reps):
+                ffi.call("wst_stream_read", buf.ptr.value + (k % copies) * nbytes, nbytes, sink.ptr)
+            e1.record()
+            wk.synchronize()
+            us = e0.elapsed_ms(e1) * 1e3 / reps
+            out["stream_read_floor_cold"] = {"us_per_call": round(us, 3),
+                                             "gbs": round(nbytes / us / 1e3, 1),
+                                             "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+            out["gemv_frac_of_floor"] = round(us / out["cold"]["us_per_call"], 4)
+            del buf
         log(f"{name}: {out}")
         res[name] = out
         del qw, si, sb
@@ -441,21 +582,27 @@ def main():
     if a.config == 4:
         prefill_bench(E, wk, a.steps)
         return
+    if a.floors:
+        floors_bench(E, wk, a.config, max(a.steps, 20))
+        return
     cfg = E.QWEN7B if a.config == 3 else E.QWEN05B
     t_gen = time.perf_counter()
     g = E.Model(cfg, seed=WEIGHT_SEED)
     wk.synchronize()
     t_gen = time.perf_counter() - t_gen
 
+    ms_need = None
     if a.config == 3:
         ctx0 = 2048
-        eng = E.Engine(g, ctx0 + max(a.steps, a.warmup) + 8)
+        ms_need = ctx0 + max(a.steps, a.warmup) + 8
+        eng = E.Engine(g, max(a.max_seq, ms_need))
         eng.fill_kv(KV_SEED, ctx0)
         workload = ("config 3: Qwen2.5-7B-shape int4 hier-g32 batch=1 greedy decode, "
                     f"KV context {ctx0} -> {ctx0 + a.steps}")
     else:
         ctx0 = 512
-        eng = E.Engine(g, ctx0 + max(a.steps, a.warmup) + 8)
+        ms_need = ctx0 + max(a.steps, a.warmup) + 8
+        eng = E.Engine(g, max(a.max_seq, ms_need))
         prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], ctx0)
         eng.prefill(prompt.astype(np.int32), chunked=True)
         workload = ("config 2: Qwen2.5-0.5B-shape int4 hier-g32 batch=1 greedy decode after a "
@@ -523,6 +670,7 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights packed to int4-hier-g32 on the device; "
                 + ("seeded f16 N(0,1) KV context)" if a.config == 3 else "seeded random prompt)"),
         "config": {"workload": workload, "bytes_per_token": int(bytes_tok),
+                   "max_seq": max(a.max_seq, ms_need),
                    "hbm_gbs": round(bytes_tok * tok_s / 1e9, 1),
                    "frac_of_hbm_peak": round(bytes_tok * tok_s / 1e9 / HBM_PEAK_GBS, 4),
                    "token_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bytes_tok, 1),

@@ -153,6 +153,14 @@ wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si, const void
                                       int32_t max_seq, const void *q_norm_w,
                                       const void *k_norm_w, float eps);
 
+/* ------------------------------------------------------------ measurement */
+
+/* One launch of the library's streaming-read kernel (16-byte nontemporal
+ * loads, four in flight per lane, 8 blocks of 256 per CU) over bytes of buf
+ * (16-byte aligned); sink is 16 writable bytes. The floor a GEMV of the same
+ * bytes is compared with (bench.py --config 1). */
+wst_status_t wst_stream_read(const void *buf, size_t bytes, void *sink);
+
 /* ------------------------------------------------- no-allocation entry */
 
 /* No counterpart in the reference. For callers that cannot allocate device

@@ -13,8 +13,9 @@ told from a bug. No reference code is imported or run.
         KV caches filled with the synthetic context (seed 2) for positions
         0..2047, one seeded token at position 2048, 64 greedy tokens; plus a
         sample of the first step's logits (the top 64 and every 64th entry)
-        and the first step under the oracle's two f32 summation orders.
-        About 4 minutes to pack on 8 threads, 4 s per token.
+        and the oracle's two f32 summation orders (first-step logits and
+        their 64-token streams). About 4 minutes to pack on 8 threads, 4 s per
+        token.
   cfg4  qwen05b_qk_rescore_4096.json: the chunked-prefill configuration (0.5B
         shape, QK-norm, fp16 head rescore of the top 32), a seeded 4096-token
         prompt, then 64 greedy tokens.
@@ -84,11 +85,13 @@ def golden_7b():
         st.pos = ctx
         return st
 
-    drift = {}
+    drift, variant_tokens = {}, {}
     for name, acc in (("f32_seq", O.ACC_F32_SEQ), ("f32_lane", O.ACC_F32_LANE)):
         with O.variant(acc):
             st = state()
-            drift[name] = st.step(first)[1].astype(np.float64)
+            nxt_v, lg_v = st.step(first)
+            drift[name] = lg_v.astype(np.float64)
+            variant_tokens[name] = _decode(st, nxt_v, lg_v, N_NEW)[0]
             st.close()
     st = state()
     nxt, lg = st.step(first)
@@ -103,6 +106,10 @@ def golden_7b():
                 oracle="mirrored",
                 first_step_logits=dict(index=[int(i) for i in sample],
                                        value=[float(lg0[i]) for i in sample]),
+                # the same stream from the oracle with only its f32 summation
+                # order changed (two ways): where these leave the mirrored
+                # stream, the reference's own freedom of order decides the token
+                order_variant_tokens=variant_tokens,
                 first_step_order_drift=dict(
                     f32_seq_vs_f32_lane=float(np.max(np.abs(drift["f32_seq"] - drift["f32_lane"]))),
                     mirrored_vs_f32_seq=float(np.max(np.abs(lg0 - drift["f32_seq"]))),

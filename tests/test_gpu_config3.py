@@ -20,7 +20,8 @@ of their sums already differ by more than that (tests/test_oracle_drift.py;
 the golden file records 0.011-0.015 on these weights), so the logit test
 asserts the GPU is no further from the oracle than 2x that order-only drift
 and reports whether the 1e-2 bar itself holds. The token stream is held to
-identical, except at an oracle near-tie.
+token identity up to the first step whose oracle top-2 margin is within twice
+that order-only drift (see the stream test).
 """
 import json
 from pathlib import Path
@@ -28,7 +29,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from conftest import assert_streams, copy_model_to_oracle
+from conftest import copy_model_to_oracle
 from whetstone_amd import engine as E
 
 pytestmark = pytest.mark.gpu
@@ -91,11 +92,34 @@ def test_7b_first_step_logits_against_oracle(orc, model7b):
     assert np.allclose(got, want, rtol=1e-3, atol=2.0 * max(order, 1e-2))
 
 
+def _first_divergence(a, b):
+    return next((i for i, (x, y) in enumerate(zip(a, b)) if int(x) != int(y)), min(len(a), len(b)))
+
+
 def test_7b_greedy_stream_matches_golden_64_steps(model7b):
-    """The benchmark's own path: the captured step graph replayed per token."""
+    """The benchmark's own path: the captured step graph replayed per token.
+
+    Token identity is the bar, with the one exception the arithmetic forces:
+    if two implementations' logits differ by at most delta everywhere, their
+    argmaxes can differ only where the top-2 margin is at most 2 delta. At
+    this depth the oracle with only its f32 summation order changed moves
+    the logits by delta = 0.0146 (the golden file's first-step figure), so a
+    first divergence is accepted only at a step whose oracle top-2 margin is
+    below 2 delta; the golden file also holds the two order variants' own
+    streams, which show where the order alone already changes the tokens."""
     eng = _engine(model7b)
     eng.capture_graph()
     got = eng.generate(np.array([GOLDEN["first_token"]], np.int32), N_NEW, chunked=False)
     eng.close()
-    n = assert_streams(got, GOLDEN["tokens"], GOLDEN["margins"])
-    print(f"7B greedy stream: {n}/{N_NEW} tokens identical to the oracle")
+    want, margins = GOLDEN["tokens"], GOLDEN["margins"]
+    assert len(got) == N_NEW
+    k = _first_divergence(got, want)
+    variants = {name: _first_divergence(toks, want)
+                for name, toks in GOLDEN["order_variant_tokens"].items()}
+    delta = GOLDEN["first_step_order_drift"]["f32_seq_vs_f32_lane"]
+    print(f"7B greedy stream: first {k}/{N_NEW} tokens identical to the oracle; the oracle's "
+          f"f32 order variants leave its stream at {variants}")
+    if k < N_NEW:
+        assert margins[k] < 2 * delta, (
+            f"diverged at step {k}: {got[k]} vs {want[k]}, oracle top-2 margin {margins[k]:.4g} "
+            f">= 2 x order-only drift {delta:.4g}")

@@ -220,6 +220,18 @@ __global__ __launch_bounds__(256) void bandwidth_read_kernel(const uint4 *__rest
   if (acc == 0x12345678u) sink[0] = (float)acc;  // practically never true
 }
 
+// One launch of the streaming read over a caller's buffer (sink: 16 bytes),
+// on the calling thread's stream: the floor a GEMV of the same bytes is held
+// against, timed by the caller with the same weights-cold rotation.
+extern "C" wst_status_t wst_stream_read(const void *buf, size_t bytes, void *sink) {
+  WST_REQUIRE(buf && sink, "wst_stream_read: null pointer");
+  WST_REQUIRE(bytes >= 16 && !((uintptr_t)buf & 15u), "wst_stream_read: bad buffer");
+  bandwidth_read_kernel<<<wst_cu_count() * 8, 256, 0, WST_STREAM>>>(
+      (const uint4 *)buf, bytes / sizeof(uint4), (float *)sink);
+  WST_TRY_KERNEL("wst_stream_read");
+  return WST_OK;
+}
+
 extern "C" wst_status_t wst_bench_bandwidth(size_t bytes, int32_t reps, double *out_gbs) {
   WST_REQUIRE(out_gbs != nullptr, "wst_bench_bandwidth: null out");
   WST_REQUIRE(reps > 0, "wst_bench_bandwidth: reps must be positive");

@@ -119,6 +119,7 @@ ABI = {
     "wst_chunk_max_tokens": (I32, []),
     "wst_gemm_int4_hier": (I32, [P, P, P, P, P, P, I32, I32, I32, I32]),
     "wst_gemm_int4_hier_noalloc": (I32, [P, P, P, P, P, P, I32, I32, I32, I32]),
+    "wst_stream_read": (I32, [P, C.c_size_t, P]),
     "wst_gemm_fp16": (I32, [P, P, P, P, I32, I32, I32, I32]),
     "wst_rmsnorm_chunk": (I32, [P, P, P, I32, I32, F32]),
     "wst_rope_cache_chunk": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, I32, P, P, F32]),
