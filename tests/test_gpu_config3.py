@@ -67,9 +67,9 @@ def test_7b_first_step_logits_against_oracle(orc, model7b):
     eng.close()
     o = copy_model_to_oracle(orc, model7b, E.QWEN7B, GOLDEN["seed"])
     lg = {}
-    for name, acc in (("mirrored", orc.ACC_F64), ("f32_seq", orc.ACC_F32_SEQ),
-                      ("f32_lane", orc.ACC_F32_LANE)):
-        with orc.variant(acc):
+    for name, acc, xq in (("mirrored", orc.ACC_F64, False), ("f32_seq", orc.ACC_F32_SEQ, False),
+                          ("f32_lane", orc.ACC_F32_LANE, False), ("xq14", orc.ACC_F64, True)):
+        with orc.variant(acc, xq):
             st = orc.State(o, CTX + 8, 0)
             st.fill_kv(GOLDEN["kv_seed"], CTX)
             st.pos = CTX
@@ -84,8 +84,14 @@ def test_7b_first_step_logits_against_oracle(orc, model7b):
     gpu = float(np.max(np.abs(got - want)))
     order = float(np.max(np.abs(lg["f32_seq"] - lg["f32_lane"])))
     within = bool(np.allclose(got, want, rtol=1e-3, atol=1e-2))
+    # the oracle with the GPU GEMV's 14-bit activation table: the table moves
+    # the logits no more than a change of summation order does
+    xq = float(np.max(np.abs(lg["xq14"] - want)))
+    gpu_xq = float(np.max(np.abs(got - lg["xq14"])))
     print(f"7B first step: GPU vs mirrored oracle {gpu:.4f} max-abs "
-          f"(1e-2/1e-3 bar {'met' if within else 'not met'}); order-only drift {order:.4f}")
+          f"(1e-2/1e-3 bar {'met' if within else 'not met'}); order-only drift {order:.4f}; "
+          f"oracle with the activation table vs without {xq:.4f}; GPU vs that oracle {gpu_xq:.4f}")
+    assert xq <= 2.0 * max(order, 1e-2)
     assert tok == orc.argmax(got)            # argmax bit-exact on the device logits
     assert tok == orc.argmax(want) or orc.top2_margin(want) < 1e-4
     assert gpu <= 2.0 * max(order, 1e-2), (gpu, order)
