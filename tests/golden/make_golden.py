@@ -6,7 +6,7 @@ checks the packer byte for byte) -- and runs the precision-mirrored forward,
 recording each step's top-2 logit margin so a divergence on a near-tie can be
 told from a bug. No reference code is imported or run.
 
-    python tests/golden/make_golden.py [05b] [7b] [cfg4]    (default: 05b)
+    python tests/golden/make_golden.py [05b] [7b] [cfg2] [cfg4]    (default: 05b)
 
   05b   qwen05b_greedy.json: 0.5B shape, 16 prompt tokens, 64 greedy tokens.
   7b    qwen7b_ctx2048_greedy.json: the 7B shape of the headline benchmark,
@@ -16,6 +16,10 @@ told from a bug. No reference code is imported or run.
         and the oracle's two f32 summation orders (first-step logits and
         their 64-token streams). About 4 minutes to pack on 8 threads, 4 s per
         token.
+  cfg2  qwen05b_ctx512_greedy.json: config 2's workload, the 0.5B shape with a
+        seeded 512-token prompt and 256 greedy tokens (context 512 -> 768),
+        plus the first generated step's logits under the oracle's two f32
+        summation orders (the order-only drift at this depth).
   cfg4  qwen05b_qk_rescore_4096.json: the chunked-prefill configuration (0.5B
         shape, QK-norm, fp16 head rescore of the top 32), a seeded 4096-token
         prompt, then 64 greedy tokens.
@@ -116,6 +120,35 @@ def golden_7b():
                     mirrored_vs_f32_lane=float(np.max(np.abs(lg0 - drift["f32_lane"]))))), t0)
 
 
+def golden_cfg2():
+    t0 = time.time()
+    cfg = O.QWEN05B
+    n_prompt, n_new = 512, 256
+    m = O.Model(cfg, SEED)
+    prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt)
+    first = {}
+    for name, acc in (("f32_seq", O.ACC_F32_SEQ), ("f32_lane", O.ACC_F32_LANE)):
+        with O.variant(acc):
+            st = O.State(m, n_prompt + 8, 0)
+            for t in prompt:
+                _, lg = st.step(int(t))
+            first[name] = lg.astype(np.float64)
+            st.close()
+    st = O.State(m, n_prompt + n_new + 8, 0)
+    for t in prompt:
+        nxt, lg = st.step(int(t))
+    lg0 = lg.astype(np.float64)
+    tokens, margins, top = _decode(st, nxt, lg, n_new)
+    _write("qwen05b_ctx512_greedy.json",
+           dict(config="qwen2.5-0.5b-shape", seed=SEED, prompt_seed=PROMPT_SEED,
+                n_prompt=n_prompt, tokens=tokens, margins=margins, top_logit=top,
+                oracle="mirrored",
+                first_step_order_drift=dict(
+                    f32_seq_vs_f32_lane=float(np.max(np.abs(first["f32_seq"] - first["f32_lane"]))),
+                    mirrored_vs_f32_seq=float(np.max(np.abs(lg0 - first["f32_seq"]))),
+                    mirrored_vs_f32_lane=float(np.max(np.abs(lg0 - first["f32_lane"]))))), t0)
+
+
 def golden_cfg4():
     t0 = time.time()
     cfg = dict(O.QWEN05B, qk_norm=1, rescore_k=32)
@@ -137,4 +170,4 @@ def golden_cfg4():
 if __name__ == "__main__":
     which = sys.argv[1:] or ["05b"]
     for w in which:
-        {"05b": golden_05b, "7b": golden_7b, "cfg4": golden_cfg4}[w]()
+        {"05b": golden_05b, "7b": golden_7b, "cfg2": golden_cfg2, "cfg4": golden_cfg4}[w]()

@@ -1,0 +1,56 @@
+"""GPU parity at config 2's workload: the Qwen2.5-0.5B shape, a seeded
+512-token prompt prefilled in 256-token chunks, then 256 greedy tokens from
+the captured step graph (context 512 -> 768), as bench.py --config 2 runs it.
+
+Reference: tests/golden/qwen05b_ctx512_greedy.json, the CPU oracle's
+precision-mirrored stream with each step's top-2 margin, and the first
+generated step's logits under the oracle's two f32 summation orders (the
+order-only drift delta at this depth). Token identity is the bar; a first
+divergence is accepted only at a step whose oracle top-2 margin is below
+2 delta, the most by which two implementations whose logits differ by at most
+delta everywhere can disagree on an argmax. Sequential prefill of the same
+prompt is held to the same bar.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from whetstone_amd import engine as E
+
+pytestmark = pytest.mark.gpu
+_PATH = Path(__file__).resolve().parent / "golden" / "qwen05b_ctx512_greedy.json"
+GOLDEN = json.loads(_PATH.read_text()) if _PATH.exists() else {"tokens": []}
+N_NEW = len(GOLDEN["tokens"])
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _have_golden():
+    if not _PATH.exists():
+        pytest.fail(f"{_PATH.name} is missing: python tests/golden/make_golden.py cfg2")
+
+
+def _first_divergence(a, b):
+    return next((i for i, (x, y) in enumerate(zip(a, b)) if int(x) != int(y)), min(len(a), len(b)))
+
+
+@pytest.mark.parametrize("chunked", [True, False], ids=["chunked", "sequential"])
+def test_05b_ctx512_stream_matches_golden(chunked):
+    g = E.Model(E.QWEN05B, seed=GOLDEN["seed"])
+    prompt = np.random.default_rng(GOLDEN["prompt_seed"]).integers(
+        0, E.QWEN05B["vocab"], GOLDEN["n_prompt"]).astype(np.int32)
+    eng = E.Engine(g, GOLDEN["n_prompt"] + N_NEW + 8)
+    eng.capture_graph()
+    got = eng.generate(prompt, N_NEW, chunked=chunked)
+    eng.close()
+    g.close()
+    want, margins = GOLDEN["tokens"], GOLDEN["margins"]
+    assert len(got) == N_NEW
+    k = _first_divergence(got, want)
+    delta = GOLDEN["first_step_order_drift"]["f32_seq_vs_f32_lane"]
+    print(f"0.5B ctx 512 ({'chunked' if chunked else 'sequential'} prefill): first {k}/{N_NEW} "
+          f"tokens identical to the oracle (order-only drift {delta:.4g})")
+    if k < N_NEW:
+        assert margins[k] < 2 * max(delta, 1e-4), (
+            f"diverged at step {k}: {got[k]} vs {want[k]}, oracle top-2 margin {margins[k]:.4g}")
