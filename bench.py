@@ -75,6 +75,8 @@ def parse():
     p.add_argument("--max-seq", type=int, default=0,
                    help="KV-cache capacity for configs 2 and 3 (default: the context plus the "
                         "generated tokens plus 8); attention's grid covers the capacity")
+    p.add_argument("--gemm-7b", action="store_true",
+                   help="with --config 4: also time the chunk GEMMs at the 7B shapes")
     p.add_argument("--floors", action="store_true",
                    help="with --config 2 or 3: the step's launch structure replayed as a graph "
                         "of plain streaming reads of each kernel's bytes (the floor of that "
@@ -262,7 +264,40 @@ def cpu_leg(g, cfg, ctx0, first_token, gpu_tokens, gpu_logits0, budget_s, same_c
     return base, check
 
 
-def prefill_bench(E, wk, n_new: int) -> None:
+def chunk_gemm_times(wk, shapes, n: int = 256, reps: int = 50) -> dict:
+    """HIP-event time of each chunk GEMM form over n tokens (weights packed on
+    the device, x f16 N(0,1)): name -> (us per call, TFLOP/s counted)."""
+    from whetstone_amd import ffi
+    out = {}
+    for name, (kind, in_f, rows) in shapes.items():
+        qw = wk.DeviceBuffer(rows * in_f // 8, np.uint32)
+        si = wk.DeviceBuffer(rows * in_f // 32, np.uint8)
+        sb = wk.DeviceBuffer(rows, np.uint32)
+        ffi.call("wst_fixture_pack_hier", qw.ptr, si.ptr, sb.ptr, in_f, 0, rows, WEIGHT_SEED, 7, 0.02)
+        x = wk.DeviceBuffer(n * in_f, np.float16)
+        ffi.call("wst_fixture_normal_f16", x.ptr, n * in_f, KV_SEED, 8, 0, 1.0, 0.0)
+        y = wk.DeviceBuffer(n * rows, np.float32)
+        if kind == "swiglu":
+            fn = lambda: ffi.call("wst_gemm_hier_swiglu_chunk", qw.ptr, si.ptr, sb.ptr, x.ptr, y.ptr,
+                                  in_f, rows // 2, n)
+        else:
+            fn = lambda: ffi.call("wst_gemm_int4_hier", qw.ptr, si.ptr, sb.ptr, x.ptr, None, y.ptr,
+                                  in_f, rows, n, 1)
+        for _ in range(5):
+            fn()
+        e0, e1 = wk.Event(), wk.Event()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        wk.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / reps
+        out[name] = {"us": round(us, 2), "tflops": round(2 * n * in_f * rows / us / 1e6, 1)}
+        del qw, si, sb, x, y
+    return out
+
+
+def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False) -> None:
     """Config 4: chunked prefill of 4096 tokens (256 per chunk), then n_new
     graph decode steps (none, and no graph capture, for n_new = 0)."""
     cfg = dict(E.QWEN05B, qk_norm=1, rescore_k=32)
@@ -301,6 +336,15 @@ def prefill_bench(E, wk, n_new: int) -> None:
             eng.token()
         wk.synchronize()
         dt_d = time.perf_counter() - t0
+    shapes = {"0.5b gate_up+swiglu": ("swiglu", H, 2 * I), "0.5b down": ("gemm", I, H),
+              "0.5b qkv": ("gemm", H, (nq + 2 * nkv) * hd), "0.5b o": ("gemm", nq * hd, H)}
+    if gemm_7b:
+        c7 = E.QWEN7B
+        H7, I7 = c7["hidden"], c7["inter"]
+        shapes.update({"7b gate_up+swiglu": ("swiglu", H7, 2 * I7), "7b down": ("gemm", I7, H7),
+                       "7b qkv": ("gemm", H7, (c7["n_q"] + 2 * c7["n_kv"]) * c7["head_dim"]),
+                       "7b o": ("gemm", c7["n_q"] * c7["head_dim"], H7)})
+    gemms = chunk_gemm_times(wk, shapes, chunk)
     line = {
         "metric": "chunked prefill tok/s (config 4)", "value": round(n_prompt / dt_p, 1),
         "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "dtype": "int4xf16->f32",
@@ -313,7 +357,8 @@ def prefill_bench(E, wk, n_new: int) -> None:
                    "prefill_tflops": round(flops / dt_p / 1e12, 2),
                    "prefill_flops": flops,
                    "decode_steps": n_new,
-                   "decode_tok_s": round(n_new / dt_d, 1) if dt_d else None},
+                   "decode_tok_s": round(n_new / dt_d, 1) if dt_d else None,
+                   "chunk_gemms_256_tokens": gemms},
     }
     eng.close()
     g.close()
@@ -580,7 +625,7 @@ def main():
         gemv_bench(wk, max(a.steps, 200))
         return
     if a.config == 4:
-        prefill_bench(E, wk, a.steps)
+        prefill_bench(E, wk, a.steps, a.gemm_7b)
         return
     if a.floors:
         floors_bench(E, wk, a.config, max(a.steps, 20))
