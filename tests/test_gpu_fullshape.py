@@ -146,3 +146,46 @@ def test_fp16_head_gemv_full_05b_shape(orc, wk):
         cur = wk.DeviceCursor(tok)
         ffi.call("wst_embed_fp16", w.ptr, cur.buf.ptr, out.ptr, in_f, out_f)
         assert np.array_equal(out.numpy(), table[row].astype(np.float32)), tok
+
+
+@pytest.mark.parametrize("k", [32, 64])
+def test_head_rescore_full_05b_shape_against_oracle(orc, wk, k):
+    """The config-4 head: the int4 logits of the 0.5B tied head (896 -> 151936)
+    from the device GEMV, then the fused rescore from the fp16 copy (top k)
+    against the oracle's ladder (orc_head_threshold, head_rescore.cu:62-180)
+    and its f64 rescore of every row at or above the threshold
+    (orc_head_rescore): the same threshold and count, rows below it
+    untouched, rescored rows within f32 rounding of the f64 dot product."""
+    in_f, vocab = 896, 151936
+    w32 = wk.DeviceBuffer(vocab * in_f, np.float32)
+    ffi.call("wst_fixture_normal_f32", w32.ptr, vocab * in_f, 0, 91, 0, 0.02)
+    head16 = wk.DeviceBuffer(vocab * in_f, np.float16)  # the fp16 copy of the same weights
+    ffi.call("wst_fixture_normal_f16", head16.ptr, vocab * in_f, 0, 91, 0, 0.02, 0.0)
+    qw = wk.DeviceBuffer(vocab * in_f // 8, np.uint32)
+    si = wk.DeviceBuffer(vocab * in_f // 32, np.uint8)
+    sb = wk.DeviceBuffer(vocab, np.uint32)
+    ffi.call("wst_quantize_int4_hier", w32.ptr, qw.ptr, si.ptr, sb.ptr, in_f, vocab)
+    del w32
+    xb = _x(orc, in_f, 92)
+    xd = dev_f16(wk, xb)
+    lg = wk.DeviceBuffer(vocab, np.float32)
+    ffi.call("wst_gemv_int4_hier_ex", qw.ptr, si.ptr, sb.ptr, xd.ptr, None, lg.ptr, in_f, vocab, 0)
+    approx = lg.numpy().copy()
+    rs = wk.HeadRescore(head16, vocab, in_f, k)
+    ffi.call("wst_head_rescore_fused", head16.ptr, xd.ptr, lg.ptr, vocab, in_f, k, rs.cap,
+             rs.scratch.ptr, rs.nblocks)
+    got = lg.numpy()
+    th, cnt, _ = orc.head_threshold(approx, k, rs.cap)
+    assert k <= cnt <= rs.cap
+    want = approx.copy()
+    hb = head16.numpy().view(np.uint16)
+    orc.lib().orc_head_rescore(np.ascontiguousarray(hb), np.ascontiguousarray(xb), want, vocab,
+                               in_f, np.float32(th))
+    sel = approx >= th
+    assert int(sel.sum()) == cnt
+    np.testing.assert_array_equal(got[~sel], approx[~sel])
+    rows = np.nonzero(sel)[0]
+    h = orc.f16_value(hb.reshape(vocab, in_f)[rows].ravel()).astype(np.float64).reshape(-1, in_f)
+    scale = np.abs(h) @ np.abs(orc.f16_value(xb).astype(np.float64))
+    assert np.all(np.abs(got[sel].astype(np.float64) - want[sel]) <= 1e-5 * scale + 1e-6)
+    assert int(np.argmax(got)) == int(np.argmax(want))
