@@ -123,6 +123,36 @@ wst_status_t wst_gemv_hier_attn(const void *qw, const void *si, const void *sb,
                                 const void *partials, void *y, int32_t n_q, int32_t head_dim,
                                 const void *pos, int32_t max_seq, int32_t out_f, int32_t accum);
 
+/* The int4-hier GEMV's activation table, built once by the producer of the
+ * GEMV's input instead of by every block of the GEMV. For an f16 vector of
+ * in_f values (in_f a multiple of 32) the table is in_f / 32 entries of 80
+ * bytes (20 u32: per group of 32 values its 14-bit fixed-point digits for
+ * v_dot8, 8*sum, the sum as f32 and the group scale; word 19 unused). The
+ * forms below write or read it; each gives the same bits as the form
+ * without it. */
+wst_status_t wst_hier_xq_table(const void *x, void *table, int32_t in_f);
+
+/* wst_gemv_int4_hier_ex with the input's table (from wst_hier_xq_table or a
+ * producer below) in place of x. */
+wst_status_t wst_gemv_hier_xq(const void *qw, const void *si, const void *sb,
+                              const void *table, const void *bias, void *y, int32_t in_f,
+                              int32_t out_f, int32_t accum);
+
+/* wst_gemv_hier_swiglu that also writes the table of out (inter / 32 entries;
+ * inter a multiple of 32): the down projection's input. */
+wst_status_t wst_gemv_hier_swiglu_xq(const void *qw, const void *si, const void *sb,
+                                     const void *x, const void *norm_w, float eps, void *out,
+                                     void *table, int32_t in_f, int32_t inter);
+
+/* wst_attn_decode_fused whose merge also writes the table of out
+ * (n_q * head_dim / 32 entries): the o projection's input. */
+wst_status_t wst_attn_decode_fused_xq(void *qkv, void *k_cache, void *v_cache,
+                                      const void *cos_tab, const void *sin_tab, void *partials,
+                                      void *out, void *table, int32_t n_q, int32_t n_kv,
+                                      int32_t head_dim, const void *pos, int32_t max_seq,
+                                      float scale, const void *q_norm_w, const void *k_norm_w,
+                                      float eps);
+
 /* Chunk (prefill) fused forms, each bit-identical to the unfused ABI sequence
  * it replaces (tested so):
  *

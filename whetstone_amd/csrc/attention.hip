@@ -37,6 +37,7 @@
 //   bit-identical to wst_rope_cache followed by wst_attn_decode.
 // * Deterministic: every sum runs in a fixed order.
 #include "common.hpp"
+#include "hier_xq.hpp"
 
 #include <stdlib.h>
 
@@ -417,9 +418,11 @@ __global__ __launch_bounds__(32 * NL) void attn_merge_kernel(const float *__rest
                                                          uint16_t *__restrict__ out, int n_q,
                                                          int hd, int nsplit,
                                                          const int32_t *__restrict__ pos_dev,
-                                                         int max_seq, int P) {
+                                                         int max_seq, int P,
+                                                         uint32_t *__restrict__ tw) {
   constexpr int B = ATTN_MERGE_BATCH;
   __shared__ float hx[NL][32][3];
+  __shared__ uint16_t mo[32];
   const int h = blockIdx.x, d0 = blockIdx.y * 32, tid = threadIdx.x;
   const int j = tid >> 5, d = d0 + (tid & 31);
   const float *pacc = partials;
@@ -484,7 +487,20 @@ __global__ __launch_bounds__(32 * NL) void attn_merge_kernel(const float *__rest
     }
     __syncthreads();
   }
-  if (j == 0) out[(size_t)h * hd + d] = f2h(st.a / st.den);
+  if (j == 0) {
+    const uint16_t v = f2h(st.a / st.den);
+    out[(size_t)h * hd + d] = v;
+    mo[tid] = v;
+  }
+  if (tw) {  // the block's 32 outputs are one group of the consumer's table
+    __syncthreads();
+    if (tid < 4) {
+      uint16_t hv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hv[e] = mo[8 * tid + e];
+      build_xq(hv, (h * hd + d0) / 8 + tid, true, tw);
+    }
+  }
 }
 
 template <int HD, int P, bool ROPE>
@@ -507,7 +523,8 @@ static void attn_go(const dim3 grid, const void *qkv, void *k_cache, void *v_cac
 template <bool ROPE>
 static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_cache,
                         void *partials, void *out, int n_q, int n_kv, const void *pos,
-                        int max_seq, float scale, const RopeArgs &ra, bool merge = true) {
+                        int max_seq, float scale, const RopeArgs &ra, bool merge = true,
+                        uint32_t *tw = nullptr) {
   const int P = wst_attn_slice_len(head_dim, max_seq);
   const int nsplit = (max_seq + P - 1) / P;
   const dim3 grid(n_kv, nsplit, attn_head_groups(n_q / n_kv));
@@ -538,13 +555,13 @@ static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_ca
     uint16_t *o = (uint16_t *)out;
     if (nsplit <= 8)
       attn_merge_kernel<2, false><<<mg, 64, 0, WST_STREAM>>>(pa, o, n_q, head_dim, nsplit, pp,
-                                                               max_seq, P);
+                                                               max_seq, P, tw);
     else if (nsplit <= 2 * ATTN_MERGE_BATCH)
       attn_merge_kernel<2, true><<<mg, 64, 0, WST_STREAM>>>(pa, o, n_q, head_dim, nsplit, pp,
-                                                              max_seq, P);
+                                                              max_seq, P, tw);
     else
       attn_merge_kernel<ATTN_MERGE_LANES, true><<<mg, 32 * ATTN_MERGE_LANES, 0, WST_STREAM>>>(
-          pa, o, n_q, head_dim, nsplit, pp, max_seq, P);
+          pa, o, n_q, head_dim, nsplit, pp, max_seq, P, tw);
   }
 }
 
@@ -612,6 +629,30 @@ extern "C" wst_status_t wst_attn_decode_fused(void *qkv, void *k_cache, void *v_
   attn_launch<true>(head_dim, qkv, k_cache, v_cache, partials, out, n_q, n_kv, pos, max_seq,
                     scale, ra);
   WST_TRY_KERNEL("wst_attn_decode_fused");
+  return WST_OK;
+}
+
+// wst_attn_decode_fused whose merge also writes the activation table of
+// its output (n_q * head_dim / 32 entries, as wst_hier_xq_table(out) writes
+// them) for the GEMV that consumes it (wst_gemv_hier_xq).
+extern "C" wst_status_t wst_attn_decode_fused_xq(void *qkv, void *k_cache, void *v_cache,
+                                                 const void *cos_tab, const void *sin_tab,
+                                                 void *partials, void *out, void *table,
+                                                 int32_t n_q, int32_t n_kv, int32_t head_dim,
+                                                 const void *pos, int32_t max_seq, float scale,
+                                                 const void *q_norm_w, const void *k_norm_w,
+                                                 float eps) {
+  const wst_status_t st =
+      attn_check(qkv, k_cache, v_cache, partials, out, n_q, n_kv, head_dim, pos, max_seq);
+  if (st != WST_OK) return st;
+  WST_REQUIRE(cos_tab && sin_tab, "wst_attn_decode_fused_xq: null rope table");
+  WST_REQUIRE(table && !((uintptr_t)table & 15u), "wst_attn_decode_fused_xq: table must be non-null and 16-byte aligned");
+  WST_REQUIRE(head_dim <= 128, "wst_attn_decode_fused_xq: head_dim must be 64 or 128");
+  const RopeArgs ra{(const float *)cos_tab, (const float *)sin_tab, (const uint16_t *)q_norm_w,
+                    (const uint16_t *)k_norm_w, eps};
+  attn_launch<true>(head_dim, qkv, k_cache, v_cache, partials, out, n_q, n_kv, pos, max_seq,
+                    scale, ra, true, (uint32_t *)table);
+  WST_TRY_KERNEL("wst_attn_decode_fused_xq");
   return WST_OK;
 }
 

@@ -47,6 +47,9 @@ struct wse_engine {
   int max_seq = 0, mode = WSE_STEP_FUSED, pos = 0;
   void *x = nullptr, *h = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr,
        *act = nullptr, *logits = nullptr, *token = nullptr, *pos_dev = nullptr;
+  // The int4-hier GEMV activation table of the o and down inputs, written by
+  // their producers (the attention merge, the gate|up SwiGLU) in the fused step.
+  void *xq = nullptr;
   std::vector<void *> kc, vc;
   void *partials = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
   // head rescore (rescore.rs:75-118)
@@ -302,6 +305,7 @@ static wst_status_t engine_build(wse_engine *e) {
   TRY(a.alloc(&e->attn, (size_t)c.n_q * hd * 2, true));
   TRY(a.alloc(&e->gu, 2 * I * 4, true));
   TRY(a.alloc(&e->act, I * 2, true));
+  TRY(a.alloc(&e->xq, (I > (size_t)c.n_q * hd ? I : (size_t)c.n_q * hd) / 32 * 80, true));
   TRY(a.alloc(&e->logits, V * 4, true));
   TRY(a.alloc(&e->token, 4, true));
   TRY(a.alloc(&e->pos_dev, 4, true));
@@ -462,6 +466,26 @@ static bool merge_in_o(const wse_engine *e) {
 }
 
 // WSE_HEAD_ARGMAX=0 keeps the separate argmax launch after the head GEMV.
+// The gate|up SwiGLU GEMV builds the down GEMV's activation table, so that
+// the down GEMV's blocks do not each build it (both forms give the same
+// bits). Used where the gate|up GEMV already takes rows 32 at a time (rows of
+// at most 32 groups, four per wave: the 0.5B shape); on wider rows the
+// grouping into 32-row units unbalances its grid (7B: 592 units on 512
+// blocks) by more than the down GEMV saves. WSE_XQ=0 switches it off, 1
+// forces it on every shape, 2 adds the attention merge building the o GEMV's
+// table (measured slower on the 7B shape: the build lengthens the merge).
+static int xq_mode() {
+  const char *v = getenv("WSE_XQ");
+  return v ? atoi(v) : -1;
+}
+static bool xq_on(const wse_engine *e) {
+  const wse_config_t &c = e->m->c;
+  if (e->mode != WSE_STEP_FUSED || c.inter % 32 != 0) return false;
+  const int m = xq_mode();
+  return m < 0 ? c.hidden <= 1024 : m >= 1;
+}
+static bool xq_o_on(const wse_engine *e) { return xq_on(e) && xq_mode() >= 2; }
+
 static bool head_argmax_on() {
   const char *v = getenv("WSE_HEAD_ARGMAX");
   return !(v && v[0] == '0');
@@ -476,6 +500,7 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
   const float scale = (float)(1.0 / sqrt((double)hd));
   const bool fused = e->mode == WSE_STEP_FUSED;
   const bool mio = merge_in_o(e);
+  const bool xq = xq_on(e);
 
   TRY(mk.mark(-1));
   TRY(embed_token(e));
@@ -493,6 +518,12 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
         TRY(mk.mark(WSE_STAGE_ATTN));
         TRY(wst_gemv_hier_attn(L.o.qw, L.o.si, L.o.sb, e->partials, e->x, nq, hd, e->pos_dev,
                                e->max_seq, H, 1));
+      } else if (xq_o_on(e)) {
+        TRY(wst_attn_decode_fused_xq(e->qkv, kc, vc, e->cos_tab, e->sin_tab, e->partials,
+                                     e->attn, e->xq, nq, nkv, hd, e->pos_dev, e->max_seq, scale,
+                                     L.q_norm, L.k_norm, eps));
+        TRY(mk.mark(WSE_STAGE_ATTN));
+        TRY(wst_gemv_hier_xq(L.o.qw, L.o.si, L.o.sb, e->xq, nullptr, e->x, nq * hd, H, 1));
       } else {
         TRY(wst_attn_decode_fused(e->qkv, kc, vc, e->cos_tab, e->sin_tab, e->partials, e->attn,
                                   nq, nkv, hd, e->pos_dev, e->max_seq, scale, L.q_norm, L.k_norm,
@@ -501,8 +532,12 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
         TRY(wst_gemv_int4_hier_ex(L.o.qw, L.o.si, L.o.sb, e->attn, nullptr, e->x, nq * hd, H, 1));
       }
       TRY(mk.mark(WSE_STAGE_O));
-      TRY(wst_gemv_hier_swiglu(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->x, L.post_norm, eps,
-                               e->act, H, I));
+      if (xq)
+        TRY(wst_gemv_hier_swiglu_xq(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->x, L.post_norm,
+                                    eps, e->act, e->xq, H, I));
+      else
+        TRY(wst_gemv_hier_swiglu(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->x, L.post_norm,
+                                 eps, e->act, H, I));
       TRY(mk.mark(WSE_STAGE_GATE_UP));
     } else {
       TRY(wst_rmsnorm(e->x, L.in_norm, e->h, H, eps));
@@ -521,7 +556,10 @@ static wst_status_t step_eager(wse_engine *e, Marks &mk) {
       TRY(wst_swiglu(e->gu, e->act, I));
       TRY(mk.mark(WSE_STAGE_GATE_UP));
     }
-    TRY(wst_gemv_int4_hier_ex(L.down.qw, L.down.si, L.down.sb, e->act, nullptr, e->x, I, H, 1));
+    if (fused && xq)
+      TRY(wst_gemv_hier_xq(L.down.qw, L.down.si, L.down.sb, e->xq, nullptr, e->x, I, H, 1));
+    else
+      TRY(wst_gemv_int4_hier_ex(L.down.qw, L.down.si, L.down.sb, e->act, nullptr, e->x, I, H, 1));
     TRY(mk.mark(WSE_STAGE_DOWN));
   }
   // The argmax rides on the head GEMV when nothing runs between the logits and
@@ -661,6 +699,11 @@ static wst_status_t stage_launch(wse_engine *e, int stage, int l, uint64_t *byte
                                       L.k_norm, eps);
       }
       *bytes = 2 * (uint64_t)nkv * seq * (uint64_t)hd * 2 + (uint64_t)nqkv * 4 + (uint64_t)nq * hd * 2;
+      if (xq_o_on(e))
+        return wst_attn_decode_fused_xq(e->qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab,
+                                        e->sin_tab, e->partials, e->attn, e->xq, nq, nkv, hd,
+                                        e->pos_dev, e->max_seq, (float)(1.0 / sqrt((double)hd)),
+                                        L.q_norm, L.k_norm, eps);
       return wst_attn_decode_fused(e->qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab,
                                    e->sin_tab, e->partials, e->attn, nq, nkv, hd, e->pos_dev,
                                    e->max_seq, (float)(1.0 / sqrt((double)hd)), L.q_norm,
@@ -674,13 +717,20 @@ static wst_status_t stage_launch(wse_engine *e, int stage, int l, uint64_t *byte
                                   e->max_seq, H, 1);
       }
       *bytes = L.o.bytes() + (uint64_t)nq * hd * 2 + (uint64_t)H * 8;
+      if (xq_o_on(e))
+        return wst_gemv_hier_xq(L.o.qw, L.o.si, L.o.sb, e->xq, nullptr, e->x, nq * hd, H, 1);
       return wst_gemv_int4_hier_ex(L.o.qw, L.o.si, L.o.sb, e->attn, nullptr, e->x, nq * hd, H, 1);
     case WSE_STAGE_GATE_UP:
       *bytes = L.gate_up.bytes() + (uint64_t)H * 6 + (uint64_t)I * 2;
+      if (xq_on(e))
+        return wst_gemv_hier_swiglu_xq(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->x,
+                                       L.post_norm, eps, e->act, e->xq, H, I);
       return wst_gemv_hier_swiglu(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->x, L.post_norm,
                                   eps, e->act, H, I);
     case WSE_STAGE_DOWN:
       *bytes = L.down.bytes() + (uint64_t)I * 2 + (uint64_t)H * 8;
+      if (xq_on(e))
+        return wst_gemv_hier_xq(L.down.qw, L.down.si, L.down.sb, e->xq, nullptr, e->x, I, H, 1);
       return wst_gemv_int4_hier_ex(L.down.qw, L.down.si, L.down.sb, e->act, nullptr, e->x, I, H,
                                    1);
     case WSE_STAGE_HEAD: {

@@ -44,6 +44,8 @@
 #define HIER_MAGIC 0x64006400u  // f16 1024.0 in both halves
 #define GEMV_THREADS 512
 #define XG_WORDS 20      // LDS words per group entry (18 used)
+#define SUBS_OF(rpb) ((rpb) < 32 ? 32 / (rpb) : 1)
+#define XT_CHUNKS(xb) ((5 * (xb) + 3) / 4)  // table chunks per thread for XB blocks of 8
 
 // Bit-field insert (a & m) | (b & ~m) as one v_bfi_b32: the mask lives in a
 // VGPR and the magic constant in an SGPR kernel argument. (Left to itself the
@@ -241,15 +243,17 @@ __device__ __forceinline__ float slot_sum(float v) {
 // wave, so a wave streams RPW rows at once.
 // AX: the argmax epilogue above (plain rows only).
 template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW = 1,
-          bool AM = false, bool AX = false>
+          bool AM = false, bool AX = false, bool XT = false, bool TW = false>
 __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     const uint4 *qw, const uint8_t *si,
     const uint32_t *__restrict__ sb, const void *xin,
     const uint16_t *norm_w, float eps, uint16_t *__restrict__ h_out,
     const uint16_t *__restrict__ bias, void *__restrict__ yout, int in_f, int nunits,
-    int accum, AttnIn am, ArgmaxOut ax) {
+    int accum, AttnIn am, ArgmaxOut ax, uint32_t *__restrict__ tw) {
   static_assert(!NORM || NT == NORM_THREADS, "the RMS reduction order assumes 512 threads");
   static_assert(!AX || !SWIGLU, "the argmax epilogue takes plain rows");
+  static_assert(!XT || (!NORM && !AM), "a prebuilt table replaces the activation loads");
+  static_assert(!TW || (SWIGLU && PD == 1), "the table of the output: SwiGLU rows, one unit in flight");
   constexpr int NR = SWIGLU ? 2 : 1;
   static_assert(RPW == 1 || WPR == 1, "rows share a wave only when a row is one wave or less");
   constexpr int NW = NT / 64;
@@ -262,18 +266,34 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   const int G = in_f / HGROUP, NB8 = in_f / 8;
   __shared__ float red[2][NW][NR];
   __shared__ float bred[16];
+  __shared__ uint16_t tws[TW ? 2 * RPB * SUBS_OF(RPB) : 1];  // TW: outputs of two group units
   extern __shared__ uint32_t xgt[];  // [G][XQ_WORDS]
 
   // 1. this thread's activation blocks b = tid + NT*i (and norm gains)
   float xf[NORM ? XB : 1][8];
   uint4 xh[NORM ? 1 : XB];
   uint4 nwv[NORM ? XB : 1];
+  // XT: the table itself, G entries of XQ_WORDS words (5 16-byte chunks),
+  // copied memory -> LDS by DMA (global_load_lds_dwordx4: lane l's 16 bytes
+  // land at M0 + 16 l), no registers held; in_f <= 8 * XB * NT bounds it by
+  // XTL * NT chunks (the launch sizes the LDS for that many: clamped lanes
+  // write copies of the last chunk past the table).
   // Every load below is unconditional (indices clamped, values masked): the
   // code stays straight-line, so the compiler counts the loads in flight and
   // waits for exactly the ones it needs (a load under a branch is followed by
   // a wait for everything outstanding).
+  if constexpr (XT) {
+    const uint32_t l0 = (uint32_t)(uintptr_t)xgt;
 #pragma unroll
-  for (int i = 0; i < XB; ++i) {
+    for (int i = 0; i < XT_CHUNKS(XB); ++i) {
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(l0 + 16u * (uint32_t)(wave * 64 + NT * i));
+      const uint32_t off = 16u * (uint32_t)min(tid + NT * i, G * (XQ_WORDS / 4) - 1);
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :: "s"(m0), "v"(off), "s"(xin) : "memory");
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < (XT ? 0 : XB); ++i) {
     const int b = tid + NT * i;
     if constexpr (NORM) {
       const int bc = min(b, NB8 - 1);
@@ -295,7 +315,18 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
 
   // 2. the first PD units' packed bytes
   const int stride = gridDim.x * RPB;
-  int base = blockIdx.x * RPB;
+  // First row of the block's t-th unit slot set. TW: a block takes whole
+  // groups of 32 consecutive rows (one group unit per 32 / RPB iterations,
+  // or RPB / 32 group units per iteration), so that it holds every output
+  // of a table entry; otherwise units are dealt round-robin.
+  constexpr int SUBS = RPB < 32 ? 32 / RPB : 1;
+  static_assert(!TW || 32 % RPB == 0 || RPB % 32 == 0, "whole groups per block");
+  auto row0 = [&](int t) -> int {
+    if constexpr (TW && RPB < 32)
+      return 32 * (blockIdx.x + (t / SUBS) * gridDim.x) + RPB * (t % SUBS);
+    else
+      return blockIdx.x * RPB + t * stride;
+  };
   struct Buf {
     uint4 wq[NR][NG];
     uint32_t idx[NR][NG];
@@ -319,7 +350,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     }
   };
 #pragma unroll
-  for (int i = 0; i < PD; ++i) load_unit(bufs[i], base + i * stride + rs);
+  for (int i = 0; i < PD; ++i) load_unit(bufs[i], row0(i) + rs);
 
   // 3. the RMS scale (rms_scale512's order: thread t, blocks t, t+512, ...)
   float s = 1.0f;
@@ -337,8 +368,14 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   }
 
   // 4. the table
+  if constexpr (XT) {
+    // The DMA went out before the first units' loads (2 per group and row:
+    // packed bytes and scale index); waiting for all but those many leaves
+    // the weights in flight. (The row scales may add more: a wait for less.)
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * NR * NG * PD) : "memory");
+  }
 #pragma unroll
-  for (int i = 0; i < XB; ++i) {
+  for (int i = 0; i < (XT ? 0 : XB); ++i) {
     const int b = tid + NT * i;
     uint16_t h[8];
     if constexpr (NORM) {
@@ -374,7 +411,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   // One unit from B; B is then refilled with the unit PD strides ahead, issued
   // after the compute and before the reductions and stores.
   auto process = [&](Buf &B) {
-    const int row = base + rs;
+    const int row = row0(it) + rs;
     // The epilogue's operands are fetched now, ahead of the next unit's weight
     // loads, so that waiting for them later does not wait for those too.
     float yv = 0.0f, bv = 0.0f;
@@ -421,7 +458,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       const float dm = h2f((uint16_t)(B.sbv[k] >> 16));
       lv[k] = d * as[k] - dm * am[k];
     }
-    load_unit(B, base + PD * stride + rs);
+    load_unit(B, row0(it + PD) + rs);
     float part[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) part[k] = WPR > 1 ? wave_sum(lv[k]) : slot_sum<LPR>(lv[k]);
@@ -443,7 +480,9 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     if (lr == 0 && row < nunits) {
       if constexpr (SWIGLU) {
         const float g = part[0], up = part[NR - 1];
-        ((uint16_t *)yout)[row] = f2h(g / (1.0f + __expf(-g)) * up);
+        const uint16_t a = f2h(g / (1.0f + __expf(-g)) * up);
+        ((uint16_t *)yout)[row] = a;
+        if constexpr (TW) tws[((it / SUBS) & 1) * RPB * SUBS + RPB * (it % SUBS) + rs] = a;
       } else {
         float v = part[0];
         if (bias) v += bv;
@@ -455,16 +494,30 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
         }
       }
     }
-    base += stride;
+    if constexpr (TW) {
+      // The last iteration of a group unit: its table entries (one quad of
+      // lanes per 32 outputs, as the GEMV prologue builds them).
+      if (it % SUBS == SUBS - 1) {
+        __syncthreads();
+        const uint16_t *src = tws + ((it / SUBS) & 1) * RPB * SUBS;
+        const int nq = RPB * SUBS / 8;  // quads of 8 outputs: 4 per group
+        if (tid < nq) {
+          uint16_t h[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) h[e] = src[8 * tid + e];
+          build_xq(h, row0(it - SUBS + 1) / 8 + tid, true, tw);
+        }
+      }
+    }
     ++it;
   };
   do {
 #pragma unroll
     for (int i = 0; i < PD; ++i) {
       process(bufs[i]);
-      if (PD > 1 && base >= nunits) break;
+      if (PD > 1 && row0(it) >= nunits) break;
     }
-  } while (base < nunits);
+  } while (row0(it) < nunits);
   if constexpr (AX) {
     __shared__ unsigned long long wbest[NW];
     best = wave_max_u64(best);
@@ -628,6 +681,7 @@ struct HierArgs {
   int in_f, nunits, accum;
   AttnIn am;
   ArgmaxOut ax;
+  uint32_t *tw;  // TW: the output's table
 };
 
 // Units in flight per row slot. Measured on the 7B shapes: a second buffer
@@ -644,10 +698,11 @@ static int gemv_pd_override() {
 }
 
 template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW, bool AM,
-          bool AX>
+          bool AX, bool XT, bool TW>
 static void launch_pd(const HierArgs &a) {
-  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW, AM, AX>;
-  const size_t lds = (size_t)(a.in_f / HGROUP) * XQ_WORDS * 4;
+  auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW, AM, AX, XT, TW>;
+  size_t lds = (size_t)(a.in_f / HGROUP) * XQ_WORDS * 4;
+  if (XT && lds < (size_t)XT_CHUNKS(XB) * NT * 16) lds = (size_t)XT_CHUNKS(XB) * NT * 16;
   // Resident blocks per CU for this instance and LDS size, queried once.
   static thread_local size_t q_lds = (size_t)-1;
   static thread_local int q_res = 1;
@@ -659,32 +714,39 @@ static void launch_pd(const HierArgs &a) {
     q_lds = lds;
   }
   // Persistent grid: at most k units per row slot.
+  // Rows a block takes at a time (TW: whole groups of 32).
   constexpr int RPB = NT / 64 / WPR * RPW;
-  const int cap = wst_cu_count() * q_res * RPB;
+  constexpr int PER = TW && RPB < 32 ? 32 : RPB;
+  const int cap = wst_cu_count() * q_res * PER;
   const int k = (a.nunits + cap - 1) / cap;
-  int grid = (a.nunits + k * RPB - 1) / (k * RPB);
+  int grid = (a.nunits + k * PER - 1) / (k * PER);
   if (gemv_full_grid()) {  // every resident slot, counts differing by at most one
-    const int full = wst_cu_count() * q_res, need = (a.nunits + RPB - 1) / RPB;
+    const int full = wst_cu_count() * q_res, need = (a.nunits + PER - 1) / PER;
     grid = full < need ? full : need;
   }
   kern<<<grid, NT, lds, WST_STREAM>>>(
       (const uint4 *)a.qw, (const uint8_t *)a.si, (const uint32_t *)a.sb, a.x,
       (const uint16_t *)a.norm_w, a.eps, (uint16_t *)a.h_out, (const uint16_t *)a.bias, a.y,
-      a.in_f, a.nunits, a.accum, a.am, a.ax);
+      a.in_f, a.nunits, a.accum, a.am, a.ax, a.tw);
 }
 
 template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1, bool AM = false,
-          bool AX = false>
+          bool AX = false, bool XT = false, bool TW = false>
 static void launch_q(const HierArgs &a) {
-  int pd = gemv_pd_override();
-  if (pd < 1 || pd > 4) {
-    const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR * RPW);
-    pd = a.nunits >= 8 * slots ? 2 : 1;
+  if constexpr (TW) {  // the table epilogue runs with one unit in flight
+    launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX, XT, TW>(a);
+    return;
+  } else {
+    int pd = gemv_pd_override();
+    if (pd < 1 || pd > 4) {
+      const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR * RPW);
+      pd = a.nunits >= 8 * slots ? 2 : 1;
+    }
+    if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX, XT, TW>(a);
+    else if (pd == 3) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM, AX, XT, TW>(a);
+    else if (pd == 4) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW, AM, AX, XT, TW>(a);
+    else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW, AM, AX, XT, TW>(a);
   }
-  if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX>(a);
-  else if (pd == 3) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM, AX>(a);
-  else if (pd == 4) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW, AM, AX>(a);
-  else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW, AM, AX>(a);
 }
 
 static int gemv_rpw_override() {
@@ -697,7 +759,8 @@ static int gemv_rpw_override() {
 // long rows use 1024 so a CU builds its table once.
 #define GEMV_MAX_G 1280  // groups per row handled by the table kernel
 
-template <bool NORM, bool SWIGLU, bool AM = false, bool AX = false>
+template <bool NORM, bool SWIGLU, bool AM = false, bool AX = false, bool XT = false,
+          bool TW = false>
 static bool hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
   // Rows of at most 32 groups (in_f <= 1024, e.g. the 0.5B hidden 896) share a
@@ -709,20 +772,20 @@ static bool hier_dispatch(const HierArgs &a) {
   // tok/s), so four is the default for every shape (a row's bits must not
   // depend on the output count). WST_GEMV_RPW=1|2|8 selects the others.
   const int rpw = gemv_rpw_override();
-  if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4, AM, AX>(a);
-  else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2, AM, AX>(a);
-  else if (G <= 32 && rpw == 8) launch_q<4, 1, 1, 512, NORM, SWIGLU, 8, AM, AX>(a);
-  else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4, AM, AX>(a);
-  else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU, 1, AM, AX>(a);
-  else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU, 1, AM, AX>(a);
-  else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU, 1, AM, AX>(a);
-  else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU, 1, AM, AX>(a);
+  if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4, AM, AX, XT, TW>(a);
+  else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2, AM, AX, XT, TW>(a);
+  else if (G <= 32 && rpw == 8) launch_q<4, 1, 1, 512, NORM, SWIGLU, 8, AM, AX, XT, TW>(a);
+  else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4, AM, AX, XT, TW>(a);
+  else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+  else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+  else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+  else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
   else if constexpr (NORM) {
-    if (G <= 512) launch_q<4, 2, 4, 512, NORM, SWIGLU, 1, AM, AX>(a);
+    if (G <= 512) launch_q<4, 2, 4, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
     else return false;
   } else {
-    if (G <= 640) launch_q<5, 2, 3, 1024, NORM, SWIGLU, 1, AM, AX>(a);
-    else if (G <= GEMV_MAX_G) launch_q<5, 4, 5, 1024, NORM, SWIGLU, 1, AM, AX>(a);
+    if (G <= 640) launch_q<5, 2, 3, 1024, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+    else if (G <= GEMV_MAX_G) launch_q<5, 4, 5, 1024, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
     else return false;
   }
   return true;
@@ -795,6 +858,74 @@ extern "C" wst_status_t wst_gemv_hier_swiglu(const void *qw, const void *si, con
   if (norm_w) hier_dispatch<true, true>(a);
   else hier_dispatch<false, true>(a);
   WST_TRY_KERNEL("wst_gemv_hier_swiglu");
+  return WST_OK;
+}
+
+// The activation table of an f16 vector as the GEMV prologue builds it
+// (hier_xq.hpp): G = in_f / 32 entries of XQ_WORDS words. One thread per 8
+// columns; the four of a group are a quad.
+__global__ __launch_bounds__(256) void xq_table_kernel(const uint16_t *__restrict__ x,
+                                                       uint32_t *__restrict__ table, int nb8) {
+  const int b = blockIdx.x * 256 + threadIdx.x;
+  const bool valid = b < nb8;
+  const uint4 v = *(const uint4 *)(x + (size_t)min(b, nb8 - 1) * 8);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint16_t h[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    h[2 * k] = (uint16_t)(w[k] & 0xFFFFu);
+    h[2 * k + 1] = (uint16_t)(w[k] >> 16);
+  }
+  build_xq(h, b, valid, table);
+}
+
+extern "C" wst_status_t wst_hier_xq_table(const void *x, void *table, int32_t in_f) {
+  WST_REQUIRE(x && table, "wst_hier_xq_table: null pointer");
+  WST_REQUIRE(in_f > 0 && in_f % HGROUP == 0, "wst_hier_xq_table: in_features must be a positive multiple of 32");
+  WST_REQUIRE(!(((uintptr_t)x | (uintptr_t)table) & 15u), "wst_hier_xq_table: x and table must be 16-byte aligned");
+  const int nb8 = in_f / 8;
+  xq_table_kernel<<<(nb8 + 255) / 256, 256, 0, WST_STREAM>>>((const uint16_t *)x, (uint32_t *)table, nb8);
+  WST_TRY_KERNEL("wst_hier_xq_table");
+  return WST_OK;
+}
+
+// wst_gemv_int4_hier_ex with the activation table already built (by
+// wst_hier_xq_table or a producer's epilogue) in place of x: the same bits.
+extern "C" wst_status_t wst_gemv_hier_xq(const void *qw, const void *si, const void *sb,
+                                         const void *table, const void *bias, void *y,
+                                         int32_t in_f, int32_t out_f, int32_t accum) {
+  const wst_status_t st = check_common(qw, si, sb, table, y, in_f, out_f, "wst_gemv_hier_xq");
+  if (st != WST_OK) return st;
+  const HierArgs a{qw, si, sb, table, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum, {}, {}};
+  if (!hier_dispatch<false, false, false, false, true>(a)) {
+    snprintf(wst_err_buf, sizeof(wst_err_buf), "wst_gemv_hier_xq: in_features above 40960");
+    return WST_ERR_SHAPE;
+  }
+  WST_TRY_KERNEL("wst_gemv_hier_xq");
+  return WST_OK;
+}
+
+// wst_gemv_hier_swiglu that also writes the activation table of its output
+// (inter / 32 entries of XQ_WORDS words, as wst_hier_xq_table(out) writes
+// them), so that the GEMV consuming it need not build the table. inter must
+// be a multiple of 32.
+extern "C" wst_status_t wst_gemv_hier_swiglu_xq(const void *qw, const void *si, const void *sb,
+                                                const void *x, const void *norm_w, float eps,
+                                                void *out, void *table, int32_t in_f,
+                                                int32_t inter) {
+  const wst_status_t st = check_common(qw, si, sb, x, out, in_f, inter, "wst_gemv_hier_swiglu_xq");
+  if (st != WST_OK) return st;
+  WST_REQUIRE(table, "wst_gemv_hier_swiglu_xq: null table");
+  WST_REQUIRE(inter % HGROUP == 0, "wst_gemv_hier_swiglu_xq: intermediate size must be a multiple of 32");
+  WST_REQUIRE(!((uintptr_t)table & 15u), "wst_gemv_hier_swiglu_xq: table must be 16-byte aligned");
+  WST_REQUIRE(in_f / HGROUP <= (norm_w ? 512 : GEMV_MAX_G),
+              "wst_gemv_hier_swiglu_xq: in_features above 16384 (40960 without the norm)");
+  WST_REQUIRE(!((uintptr_t)norm_w & 15u), "wst_gemv_hier_swiglu_xq: norm weight must be 16-byte aligned");
+  HierArgs a{qw, si, sb, x, norm_w, eps, nullptr, nullptr, out, in_f, inter, 0, {}, {}};
+  a.tw = (uint32_t *)table;
+  if (norm_w) hier_dispatch<true, true, false, false, false, true>(a);
+  else hier_dispatch<false, true, false, false, false, true>(a);
+  WST_TRY_KERNEL("wst_gemv_hier_swiglu_xq");
   return WST_OK;
 }
 

@@ -142,6 +142,10 @@ ABI = {
     "wst_head_rescore_fused": (I32, [P, P, P, I32, I32, I32, I32, P, I32]),
     "wst_gemm_hier_swiglu_chunk": (I32, [P, P, P, P, P, I32, I32, I32]),
     "wst_attn_decode_slices": (I32, [P, P, P, P, P, P, I32, I32, I32, P, I32, F32, P, P, F32]),
+    "wst_hier_xq_table": (I32, [P, P, I32]),
+    "wst_gemv_hier_xq": (I32, [P, P, P, P, P, P, I32, I32, I32]),
+    "wst_gemv_hier_swiglu_xq": (I32, [P, P, P, P, P, F32, P, P, I32, I32]),
+    "wst_attn_decode_fused_xq": (I32, [P, P, P, P, P, P, P, P, I32, I32, I32, P, I32, F32, P, P, F32]),
     "wst_gemv_hier_attn": (I32, [P, P, P, P, P, I32, I32, P, I32, I32, I32]),
     "wst_gemm_hier_norm_chunk": (I32, [P, P, P, P, P, P, I32, I32, I32, I32, P, F32, P]),
     "wst_gemm_hier_rope_chunk": (I32, [P, P, P, P, P, P, I32, P, P, P, P, I32, I32, I32, I32, I32,
