@@ -71,14 +71,18 @@ struct AttnShape {
 
 // Query-head groups per kv head (grid z): the heads of a kv head are split over
 // this many blocks per slice, each staging the same K/V tile, so that a slice's
-// score and P.V work is spread over more CUs. WST_ATTN_HEAD_GROUPS overrides.
-static int attn_head_groups(int gqa) {
+// score and P.V work is spread over more CUs. Every head's arithmetic is the
+// same in any group. Default: one group, or one block per head when the grid
+// would have fewer than 32 blocks (0.5B: 2 kv heads x 4 slices; attention 4.85
+// -> 4.4 us; on the 7B grid of 76 blocks two or more groups measured equal
+// or slower). WST_ATTN_HEAD_GROUPS overrides.
+static int attn_head_groups(int gqa, int blocks) {
   static int v = -1;
   if (v < 0) {
     const char *e = getenv("WST_ATTN_HEAD_GROUPS");
     v = e ? atoi(e) : 0;
   }
-  int z = v > 0 ? v : 1;
+  int z = v > 0 ? v : (blocks < 32 ? gqa : 1);
   z = z < gqa ? z : gqa;
   const int hpz = (gqa + z - 1) / z;  // heads per group; every group gets >= 1
   return (gqa + hpz - 1) / hpz;
@@ -527,7 +531,7 @@ static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_ca
                         uint32_t *tw = nullptr) {
   const int P = wst_attn_slice_len(head_dim, max_seq);
   const int nsplit = (max_seq + P - 1) / P;
-  const dim3 grid(n_kv, nsplit, attn_head_groups(n_q / n_kv));
+  const dim3 grid(n_kv, nsplit, attn_head_groups(n_q / n_kv, n_kv * nsplit));
 #define ATTN_GO(hd_, p_) attn_go<hd_, p_, ROPE>(grid, qkv, k_cache, v_cache, partials, n_q, \
                                                 n_kv, pos, max_seq, scale, ra)
   switch (head_dim * 1000 + P) {
