@@ -318,8 +318,6 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 //   0..31 of a tile are gate rows a0..a0+31 and rows 32..63 the up rows
 //   inter+a0.., and the epilogue writes act = f16(silu(gate) * up).
 #define GW_BM 64
-#define GW_BN 256
-#define GW_THREADS 512
 #define GW_KG 2
 #define GW_KC (GW_KG * HGROUP)          // 64 columns per step
 #define GW_KS (GW_KC + 8)               // W tile row stride in halves
@@ -330,48 +328,72 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 #define GW_DW 4                         // packed-weight steps in flight (registers)
 #define GW_XPAD 64                      // bytes between DMA blocks: t and t+8 on other banks
 #define GW_XWAVE (4 * (1024 + GW_XPAD)) // bytes of a wave's 32 tokens in one stage
-#define GW_XSTAGE (8 * GW_XWAVE)        // bytes of one x ring stage
-#define GW_LDS_X (GW_DX * GW_XSTAGE)
 #define GW_LDS_W (2 * GW_WT * 2)
-#define GW_LDS_C (GW_BN * GW_CS * 4)
-#define GW_LDS (GW_LDS_X + GW_LDS_W > GW_LDS_C ? GW_LDS_X + GW_LDS_W : GW_LDS_C)
-#define GW_VMCNT (2 + 6 * (GW_DX - 1))
 static_assert(GW_DW == GW_DX + 1, "the wait count assumes the weights lead x by one step");
+
+// NWV waves of 32 tokens: 256-token tiles (8 waves, one packed word per
+// thread per step) or 128-token tiles (4 waves, two words per thread) for
+// shapes whose 256-token tiles leave CUs idle.
+template <int NWV>
+struct GwShape {
+  static constexpr int THREADS = 64 * NWV;
+  static constexpr int BN = 32 * NWV;
+  static constexpr int RPT = 512 / THREADS;           // W words per thread per step
+  static constexpr int XSTAGE = NWV * GW_XWAVE;       // bytes of one x ring stage
+  static constexpr int LDS_X = GW_DX * XSTAGE;
+  static constexpr int LDS_C = BN * GW_CS * 4;
+  static constexpr int LDS = LDS_X + GW_LDS_W > LDS_C ? LDS_X + GW_LDS_W : LDS_C;
+  // Ops issued after x(st) when step st is multiplied: x and W of the steps
+  // in flight (4 DMA ops and 2 RPT weight loads per step).
+  static constexpr int VMCNT = 4 * (GW_DX - 1) + 2 * RPT * GW_DX;
+  static_assert(RPT * THREADS == 512, "64 rows x 2 groups x 4 words per step");
+};
 
 typedef float gm_f16v __attribute__((ext_vector_type(16)));
 
-template <bool HIER, bool SWI>
-__global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
+template <bool HIER, bool SWI, int NWV>
+__global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
     const void *__restrict__ w, const uint8_t *__restrict__ si, const uint32_t *__restrict__ sb,
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ bias, float *__restrict__ y,
     float *__restrict__ ws, int in_f, int out_f, int n, int accum, int gps) {
 #pragma clang fp contract(off)
   static_assert(HIER, "the wide tiles take int4-hier weights");
+  using S = GwShape<NWV>;
+  constexpr int RPT = S::RPT, THREADS = S::THREADS, BN = S::BN;
   extern __shared__ __align__(16) unsigned char gw_lds[];
   const uint32_t lds0 = (uint32_t)(uintptr_t)gw_lds;  // byte address of the ring
-  uint16_t *wt = (uint16_t *)(gw_lds + GW_LDS_X);      // [2][GW_BM][GW_KS]
+  uint16_t *wt = (uint16_t *)(gw_lds + S::LDS_X);      // [2][GW_BM][GW_KS]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: M0 takes it
-  const int r0 = blockIdx.x * GW_BM, t0 = blockIdx.y * GW_BN;
+  const int r0 = blockIdx.x * GW_BM, t0 = blockIdx.y * BN;
   const int G = in_f / HGROUP;
   const int g_begin = blockIdx.z * gps, g_end = min(G, g_begin + gps);
   const int steps = (g_end - g_begin + GW_KG - 1) / GW_KG;
 
-  // W assignment: tile row wr = tid / 8, group wg = (tid / 4) % 2 of the
-  // step, packed word ww = tid % 4 of the group (columns 8 ww .. 8 ww + 7).
-  const int wr = tid >> 3, wg = (tid >> 2) & 1, ww = tid & 3;
-  const int wrow = SWI ? (wr < 32 ? min(r0 / 2 + wr, out_f - 1)
-                                  : out_f + min(r0 / 2 + wr - 32, out_f - 1))
-                       : min(r0 + wr, out_f - 1);
-  // The row's (d, dmin), loaded with the prologue's loads (by asm, so that the
-  // compiler's own wait for it does not wait for those too).
-  uint32_t sbv;
-  asm volatile("global_load_dword %0, %1, off" : "=v"(sbv) : "v"(sb + wrow) : "memory");
-  // Byte offsets from w / si of this thread's word and index at step 0; a
-  // step adds 32 bytes (qw) and 2 (si). The group index is clamped per step.
-  const uint32_t *wq_base = (const uint32_t *)w + (size_t)wrow * (in_f / 8) + ww;
-  const uint8_t *wi_base = si + (size_t)wrow * G;
-  float d = 0.0f, dm = 0.0f;  // set once the prologue's loads land
+  // W assignment: word u = tid + THREADS j (j < RPT) is tile row wr = u / 8,
+  // group wg = (u / 4) % 2 of the step, packed word ww = u % 4 of the group
+  // (columns 8 ww .. 8 ww + 7).
+  const int wg = (tid >> 2) & 1, ww = tid & 3;
+  int wr[RPT];
+  uint32_t sbv[RPT];
+  const uint32_t *wq_base[RPT];
+  const uint8_t *wi_base[RPT];
+  float d[RPT], dm[RPT];  // set once the prologue's loads land
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    wr[j] = (tid + THREADS * j) >> 3;
+    const int wrow = SWI ? (wr[j] < 32 ? min(r0 / 2 + wr[j], out_f - 1)
+                                       : out_f + min(r0 / 2 + wr[j] - 32, out_f - 1))
+                         : min(r0 + wr[j], out_f - 1);
+    // The row's (d, dmin), loaded with the prologue's loads (by asm, so that
+    // the compiler's own wait for it does not wait for those too).
+    asm volatile("global_load_dword %0, %1, off" : "=v"(sbv[j]) : "v"(sb + wrow) : "memory");
+    // This word's and index's addresses at step 0; a step adds 32 bytes (qw)
+    // and 2 (si). The group index is clamped per step.
+    wq_base[j] = (const uint32_t *)w + (size_t)wrow * (in_f / 8) + ww;
+    wi_base[j] = si + (size_t)wrow * G;
+    d[j] = dm[j] = 0.0f;
+  }
 
   // x DMA: instruction i of wave `wave` covers tokens 8i .. 8i+7 of the wave's
   // 32; lane l loads token 8i + l/8, chunk (l % 8) ^ (token % 8).
@@ -388,7 +410,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
   auto issue_x = [&](int step) {  // 4 DMA ops
     step = min(step, steps - 1);
     const int col = min((g_begin + step * GW_KG) * HGROUP, in_f - GW_KC);
-    const uint32_t stage = wave_x + (uint32_t)(step % GW_DX) * GW_XSTAGE;
+    const uint32_t stage = wave_x + (uint32_t)(step % GW_DX) * S::XSTAGE;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t m0 = stage + (uint32_t)i * (1024u + GW_XPAD);
@@ -397,29 +419,45 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
                    :: "s"(m0), "v"(off), "s"(x) : "memory");
     }
   };
-  uint32_t wq[GW_DW], wi[GW_DW];
-  auto issue_w = [&](int step, uint32_t &q, uint32_t &ix) {  // 2 ops
+  uint32_t wq[GW_DW][RPT], wi[GW_DW][RPT];
+  auto issue_w = [&](int step, uint32_t (&q)[RPT], uint32_t (&ix)[RPT]) {  // 2 RPT ops
     step = min(step, steps - 1);
     const int g = min(g_begin + step * GW_KG + wg, G - 1);
-    const uint32_t *qa = wq_base + (size_t)g * 4;
-    const uint8_t *ia = wi_base + g;
-    asm volatile("global_load_dword %0, %1, off" : "=v"(q) : "v"(qa) : "memory");
-    asm volatile("global_load_ubyte %0, %1, off" : "=v"(ix) : "v"(ia) : "memory");
-  };
-  auto store_w = [&](uint32_t q, uint32_t ix, int step, int buf) {
-    const bool live = g_begin + step * GW_KG + wg < g_end;
-    const float s = live ? __fmul_rn(d, (float)(ix & 0xFu)) : 0.0f;
-    const float m = live ? __fmul_rn(-dm, (float)((ix >> 4) & 0xFu)) : 0.0f;
-    uint32_t hv[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float lo = __builtin_fmaf((float)((q >> (8 * k)) & 0xFu), s, m);
-      const float hi = __builtin_fmaf((float)((q >> (8 * k + 4)) & 0xFu), s, m);
-      hv[k] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+    for (int j = 0; j < RPT; ++j) {
+      const uint32_t *qa = wq_base[j] + (size_t)g * 4;
+      const uint8_t *ia = wi_base[j] + g;
+      asm volatile("global_load_dword %0, %1, off" : "=v"(q[j]) : "v"(qa) : "memory");
+      asm volatile("global_load_ubyte %0, %1, off" : "=v"(ix[j]) : "v"(ia) : "memory");
     }
-    *(gm_u4 *)(wt + buf * GW_WT + wr * GW_KS + wg * HGROUP + 8 * ww) =
-        (gm_u4){hv[0], hv[1], hv[2], hv[3]};
   };
+  auto store_w = [&](const uint32_t (&q)[RPT], const uint32_t (&ix)[RPT], int step, int buf) {
+    const bool live = g_begin + step * GW_KG + wg < g_end;
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const float s = live ? __fmul_rn(d[j], (float)(ix[j] & 0xFu)) : 0.0f;
+      const float m = live ? __fmul_rn(-dm[j], (float)((ix[j] >> 4) & 0xFu)) : 0.0f;
+      uint32_t hv[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float lo = __builtin_fmaf((float)((q[j] >> (8 * k)) & 0xFu), s, m);
+        const float hi = __builtin_fmaf((float)((q[j] >> (8 * k + 4)) & 0xFu), s, m);
+        hv[k] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+      }
+      *(gm_u4 *)(wt + buf * GW_WT + wr[j] * GW_KS + wg * HGROUP + 8 * ww) =
+          (gm_u4){hv[0], hv[1], hv[2], hv[3]};
+    }
+  };
+  // Wait until at most `n` ops are outstanding; the registers of W ring slot
+  // `u` are operands, so that no use of them is scheduled above the wait.
+#define GW_WAIT(u, n_)                                                               \
+  if constexpr (RPT == 1)                                                            \
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(wq[u][0]), "+v"(wi[u][0])              \
+                 : "n"(n_) : "memory");                                              \
+  else                                                                               \
+    asm volatile("s_waitcnt vmcnt(%4)"                                               \
+                 : "+v"(wq[u][0]), "+v"(wi[u][0]), "+v"(wq[u][RPT - 1]), "+v"(wi[u][RPT - 1]) \
+                 : "n"(n_) : "memory");
 
   gm_f16v acc[2];  // [row tile]
 #pragma unroll
@@ -432,7 +470,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
   const uint32_t xrow0 = (uint32_t)(l32 >> 3) * (1024u + GW_XPAD) + (uint32_t)(l32 & 7) * 128u;
   auto compute = [&](int step) {
     const uint16_t *wb = wt + (step & 1) * GW_WT + l32 * GW_KS + 8 * kh;
-    const unsigned char *xs = gw_lds + (wave_x - lds0) + (uint32_t)(step % GW_DX) * GW_XSTAGE + xrow0;
+    const unsigned char *xs = gw_lds + (wave_x - lds0) + (uint32_t)(step % GW_DX) * S::XSTAGE + xrow0;
 #pragma unroll
     for (int k = 0; k < GW_NKK; ++k) {
       const int c = 2 * k + kh;
@@ -453,11 +491,20 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
     issue_x(q);
     issue_w(q + 2, wq[q + 2], wi[q + 2]);
   }
-  // sb and W(0) are followed by 2 + 6 (GW_DX - 1) ops
-  asm volatile("s_waitcnt vmcnt(%3)" : "+v"(wq[0]), "+v"(wi[0]), "+v"(sbv) : "n"(GW_VMCNT)
-               : "memory");
-  d = h2f((uint16_t)(sbv & 0xFFFFu));
-  dm = h2f((uint16_t)(sbv >> 16));
+  // sb and W(0) are followed by S::VMCNT ops
+  if constexpr (RPT == 1)
+    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(wq[0][0]), "+v"(wi[0][0]), "+v"(sbv[0])
+                 : "n"(S::VMCNT) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%6)"
+                 : "+v"(wq[0][0]), "+v"(wi[0][0]), "+v"(wq[0][RPT - 1]), "+v"(wi[0][RPT - 1]),
+                   "+v"(sbv[0]), "+v"(sbv[RPT - 1])
+                 : "n"(S::VMCNT) : "memory");
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    d[j] = h2f((uint16_t)(sbv[j] & 0xFFFFu));
+    dm[j] = h2f((uint16_t)(sbv[j] >> 16));
+  }
   store_w(wq[0], wi[0], 0, 0);
   __syncthreads();
 
@@ -470,9 +517,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
     if (st >= steps) break;                                                     \
     issue_x(st + GW_DX - 1);                                                    \
     issue_w(st + GW_DW, wq[(U) % GW_DW], wi[(U) % GW_DW]);                      \
-    asm volatile("s_waitcnt vmcnt(%2)"                                          \
-                 : "+v"(wq[((U) + 1) % GW_DW]), "+v"(wi[((U) + 1) % GW_DW])     \
-                 : "n"(GW_VMCNT) : "memory");                                   \
+    GW_WAIT(((U) + 1) % GW_DW, S::VMCNT)                                        \
     compute(st);                                                                \
     store_w(wq[((U) + 1) % GW_DW], wi[((U) + 1) % GW_DW], st + 1, (st + 1) & 1); \
     __syncthreads();                                                            \
@@ -484,6 +529,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
     GW_STEP(3)
   }
 #undef GW_STEP
+#undef GW_WAIT
   // Clamped look-ahead DMAs may still be landing in the ring, which the
   // epilogue tile overlaps.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -491,7 +537,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
 
   // Epilogue through LDS, token-major: accumulator r of row tile a holds row
   // 32 a + 8 (r / 4) + 4 (lane / 32) + r % 4, token lane % 32 of the wave.
-  float *ct = (float *)gw_lds;  // [GW_BN][GW_CS]
+  float *ct = (float *)gw_lds;  // [BN][GW_CS]
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -504,8 +550,8 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
     uint16_t *act = (uint16_t *)y;
     const int a0 = r0 / 2;
 #pragma unroll
-    for (int j = 0; j < GW_BN * 32 / 4 / GW_THREADS; ++j) {
-      const int idx = tid + GW_THREADS * j;
+    for (int j = 0; j < BN * 32 / 4 / THREADS; ++j) {
+      const int idx = tid + THREADS * j;
       const int tl = idx / 8, kl = (idx % 8) * 4;
       const int tok = t0 + tl;
       if (tok >= n) continue;
@@ -530,8 +576,8 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_wide_kernel(
   float *dst0 = split ? ws + (size_t)blockIdx.z * n * out_f : y;
   const bool vec = (out_f & 3) == 0;
 #pragma unroll 4
-  for (int j = 0; j < GW_BM * GW_BN / 4 / GW_THREADS; ++j) {
-    const int idx = tid + GW_THREADS * j;
+  for (int j = 0; j < GW_BM * BN / 4 / THREADS; ++j) {
+    const int idx = tid + THREADS * j;
     const int tl = idx / (GW_BM / 4), rl = (idx % (GW_BM / 4)) * 4;
     const int tok = t0 + tl, row = r0 + rl;
     if (tok >= n || row >= out_f) continue;
@@ -685,33 +731,57 @@ void set_lds_attr() {
   if (!done) {
     (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<HIER, SWI>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, GM_LDS);
-    if constexpr (HIER)
-      (void)hipFuncSetAttribute((const void *)gemm_wide_kernel<HIER, SWI>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, GW_LDS);
+    if constexpr (HIER) {
+      (void)hipFuncSetAttribute((const void *)gemm_wide_kernel<HIER, SWI, 8>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, GwShape<8>::LDS);
+      (void)hipFuncSetAttribute((const void *)gemm_wide_kernel<HIER, SWI, 4>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, GwShape<4>::LDS);
+    }
     done = true;
   }
 }
 
 struct GemmPlan {
   bool wide;
+  int nwv;  // wide tiles: waves of 32 tokens (8: 256-token tiles, 4: 128)
   int bm, bn, kg;
   int splits, gps;
   dim3 grid;
 };
+
+static int gemm_bn_override() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("WST_GEMM_BN");
+    v = e ? atoi(e) : 0;
+  }
+  return v;
+}
 
 // Splits so that the grid covers the chip, each at least one step long.
 // rows: the weight matrix's row count (2 * inter for the SwiGLU form), which
 // with in_f picks the tiles: the wide tiles for long rows or many of them,
 // where their deeper pipeline pays; short K with few rows (the 0.5B qkv and
 // o projections) splits K into pieces too short for it.
-GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0) {
+GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0, bool swi = false) {
   GemmPlan p;
   if (rows <= 0) rows = out_f;
   // (The wide tiles address x with 32-bit byte offsets.)
   p.wide = hier && wide_tiles() && in_f >= GW_KC && (in_f >= 2048 || rows >= 4096) &&
            (size_t)n * in_f * 2 < ((size_t)1 << 31);
+  // Wide tiles of 128 tokens for the split-K shapes, where 256-token tiles
+  // would leave CUs without a tile: 7B qkv 43.0 -> 36.2 us, 7B down 100.3 ->
+  // 95.6 us (0.5B down unchanged). Not for the SwiGLU form, which never
+  // splits: its 128-token tiles run one wave per SIMD (0.5B gate|up 14.0 ->
+  // 16.7 us). WST_GEMM_BN=128|256 forces one.
+  p.nwv = 8;
+  if (p.wide) {
+    const int forced = gemm_bn_override();
+    const int t256 = ((out_f + GW_BM - 1) / GW_BM) * ((n + 255) / 256);
+    if (forced == 128 || (forced != 256 && !swi && n > 128 && t256 < wst_cu_count())) p.nwv = 4;
+  }
   p.bm = p.wide ? GW_BM : GM_BM;
-  p.bn = p.wide ? GW_BN : GM_BN;
+  p.bn = p.wide ? 32 * p.nwv : GM_BN;
   p.kg = p.wide ? GW_KG : GM_KG;
   const int G = in_f / HGROUP;
   const int tiles = ((out_f + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
@@ -737,9 +807,14 @@ void launch_gemm(const GemmPlan &p, const void *w, const void *si, const void *s
   set_lds_attr<HIER, SWI>();
   if constexpr (HIER) {
     if (p.wide) {
-      gemm_wide_kernel<HIER, SWI><<<p.grid, GW_THREADS, GW_LDS, WST_STREAM>>>(
-        w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
-        (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps);
+      if (p.nwv == 4)
+        gemm_wide_kernel<HIER, SWI, 4><<<p.grid, GwShape<4>::THREADS, GwShape<4>::LDS, WST_STREAM>>>(
+            w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
+            (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps);
+      else
+        gemm_wide_kernel<HIER, SWI, 8><<<p.grid, GwShape<8>::THREADS, GwShape<8>::LDS, WST_STREAM>>>(
+            w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
+            (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps);
       return;
     }
   }
@@ -821,7 +896,7 @@ extern "C" wst_status_t wst_gemm_hier_swiglu_chunk(const void *qw, const void *s
   if (st != WST_OK) return st;
   WST_REQUIRE(act, "wst_gemm_hier_swiglu_chunk: null pointer");
   // Never split: a tile pairs BM/2 gate rows with the matching up rows.
-  GemmPlan p = plan_gemm(in_f, inter, n, true, 2 * inter);
+  GemmPlan p = plan_gemm(in_f, inter, n, true, 2 * inter, true);
   p.splits = 1;
   p.gps = in_f / HGROUP;
   p.grid = dim3((inter + p.bm / 2 - 1) / (p.bm / 2), (n + p.bn - 1) / p.bn, 1);
