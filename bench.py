@@ -96,7 +96,7 @@ def parse():
 
 def _short(name: str) -> str:
     name = name.replace("HIP_vector_type<unsigned int, 4u>", "uint4")
-    return name.split("(")[0].replace("void ", "")[:72]
+    return name.split("(")[0].replace("void ", "")[:96]
 
 
 def summarize(dirs, calibration, copy_mib) -> None:
@@ -115,7 +115,7 @@ def summarize(dirs, calibration, copy_mib) -> None:
             rows = list(csv.DictReader(open(f)))
             print(f"kernel stats ({os.path.basename(f)}): name | calls | avg us | total ms | %")
             for r in rows[:16]:
-                print(f"  {_short(r['Name']):72s} | {int(r['Calls']):6d} | "
+                print(f"  {_short(r['Name']):96s} | {int(r['Calls']):6d} | "
                       f"{float(r['AverageNs']) / 1e3:9.2f} | {float(r['TotalDurationNs']) / 1e6:9.2f}"
                       f" | {float(r['Percentage']):5.1f}")
         for f in sorted(glob.glob(os.path.join(d, "*counter_collection.csv"))):
@@ -128,7 +128,7 @@ def summarize(dirs, calibration, copy_mib) -> None:
             for (cn, kn, grid), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:16]:
                 sc = scale.get(cn, 1.0)
                 avg = sum(v) / len(v)
-                print(f"  {cn} | {kn:72s} | {grid:8d} | {len(v):5d} | {avg:12.1f} | {sc:.4f} | "
+                print(f"  {cn} | {kn:96s} | {grid:8d} | {len(v):5d} | {avg:12.1f} | {sc:.4f} | "
                       f"{avg * 1024 * sc:14.0f}")
     for cn, sc in sorted(scale.items()):
         print(f"calibration: {cn} reads {1 / sc:.5f} KiB per KiB a copy kernel moves (scale {sc:.5f})")
