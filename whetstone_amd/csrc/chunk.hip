@@ -255,27 +255,44 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
     // the next tile's loads go out now (the registers above are consumed)
     const int next = kt + AC_WAVES;
     AC_LOAD_TILE(kr, vr, min(next, ntiles - 1));
-    // online softmax per token row (register i), the row spread over 16 lanes
+    // online softmax per token row (register i), the row spread over 16 lanes.
+    // A tile wholly below the block's first token's limit and the cache end
+    // (most of them) needs no mask: the same values without the selects.
     float corr[4];
+    const bool full = p0 + AC_KT - 1 <= pos0 + t0 && p0 + AC_KT <= kend;  // uniform
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int lim = pos0 + t0 + 4 * kg + i;  // last position this token attends
-      float sv[2];
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        const int p = p0 + 16 * t2 + r16;
-        sv[t2] = (p <= lim && p < kend) ? sc[t2][i] : -INFINITY;
+      for (int i = 0; i < 4; ++i) {
+        const float mx = dpp_max16(fmaxf(sc[0][i], sc[1][i]));
+        const float mn = fmaxf(m[i], mx);
+        corr[i] = (m[i] == -INFINITY) ? 0.0f : __expf(m[i] - mn);
+        const float pv0 = __expf(sc[0][i] - mn), pv1 = __expf(sc[1][i] - mn);
+        l[i] = l[i] * corr[i] + pv0 + pv1;  // this lane's columns; rows reduce at the end
+        m[i] = mn;
+        sc[0][i] = pv0;
+        sc[1][i] = pv1;
       }
-      const float mx = dpp_max16(fmaxf(sv[0], sv[1]));
-      const float mn = fmaxf(m[i], mx);
-      corr[i] = (m[i] == -INFINITY) ? 0.0f : __expf(m[i] - mn);
-      float pv[2];
+    } else {
 #pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) pv[t2] = (sv[t2] == -INFINITY) ? 0.0f : __expf(sv[t2] - mn);
-      l[i] = l[i] * corr[i] + pv[0] + pv[1];  // this lane's columns; rows reduce at the end
-      m[i] = mn;
-      sc[0][i] = pv[0];
-      sc[1][i] = pv[1];
+      for (int i = 0; i < 4; ++i) {
+        const int lim = pos0 + t0 + 4 * kg + i;  // last position this token attends
+        float sv[2];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const int p = p0 + 16 * t2 + r16;
+          sv[t2] = (p <= lim && p < kend) ? sc[t2][i] : -INFINITY;
+        }
+        const float mx = dpp_max16(fmaxf(sv[0], sv[1]));
+        const float mn = fmaxf(m[i], mx);
+        corr[i] = (m[i] == -INFINITY) ? 0.0f : __expf(m[i] - mn);
+        float pv[2];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) pv[t2] = (sv[t2] == -INFINITY) ? 0.0f : __expf(sv[t2] - mn);
+        l[i] = l[i] * corr[i] + pv[0] + pv[1];
+        m[i] = mn;
+        sc[0][i] = pv[0];
+        sc[1][i] = pv[1];
+      }
     }
     // P (hi, lo) to LDS as [pos][tok]: one 8-byte store per tile and part
 #pragma unroll
@@ -293,10 +310,15 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
       *(uint2 *)(pl + row * S::PR + 4 * kg) =
           make_uint2(lv[0] | ((uint32_t)lv[1] << 16), lv[2] | ((uint32_t)lv[3] << 16));
     }
+    // O's rescale, skipped when no row's maximum moved in the whole wave
+    // (every factor 1: the products would be exact copies).
+    const bool same = corr[0] == 1.0f && corr[1] == 1.0f && corr[2] == 1.0f && corr[3] == 1.0f;
+    if (!__all(same)) {  // some lane of the wave has a factor != 1
 #pragma clang loop unroll(full)
-    for (int t = 0; t < S::NT; ++t)
+      for (int t = 0; t < S::NT; ++t)
 #pragma clang loop unroll(full)
-      for (int i = 0; i < 4; ++i) o[t][i] *= corr[i];
+        for (int i = 0; i < 4; ++i) o[t][i] *= corr[i];
+    }
     // A operand: P[tok = r16][pos = 8kg + i]; source lane s reads row 8kg + s/4 (+4), cols 4(s%4)
     const int sr = 8 * kg + (r16 >> 2), sc4 = 4 * (r16 & 3);
     const ac_h8 pah = tr_pair(ph + sr * S::PR + sc4, ph + (sr + 4) * S::PR + sc4);
