@@ -85,7 +85,11 @@ def test_gemv_on_a_table_equals_gemv_on_x(orc, wk, in_f, out_f, bias, accum):
 
 
 @pytest.mark.parametrize("in_f,inter,norm", [(3584, 18944, True), (896, 4864, True),
-                                             (3584, 1024, True), (896, 320, False)])
+                                             (3584, 1024, True), (896, 320, False),
+                                             # rows of two waves (4 and 8 rows per block
+                                             # iteration: 8 and 4 iterations per group)
+                                             (12288, 512, True), (18944, 256, False),
+                                             (8192, 384, True), (256, 96, True)])
 def test_swiglu_xq_writes_the_table_of_its_output(orc, wk, in_f, inter, norm):
     qw = wk.DeviceBuffer(2 * inter * in_f // 8, np.uint32)
     si = wk.DeviceBuffer(2 * inter * in_f // 32, np.uint8)
