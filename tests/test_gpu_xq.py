@@ -148,3 +148,30 @@ def test_xq_entry_points_check_their_arguments(wk):
     assert ffi.lib().wst_hier_xq_table(None, t.ptr, 64) != 0
     assert ffi.lib().wst_gemv_hier_swiglu_xq(x.ptr, x.ptr, x.ptr, x.ptr, None, np.float32(1e-6),
                                              x.ptr, t.ptr, 64, 48) != 0
+
+
+@pytest.mark.parametrize("inter", [96, 160])
+def test_swiglu_xq_eight_rows_per_wave_stops_at_the_last_group(orc, wk, monkeypatch, inter):
+    """WST_GEMV_RPW=8 (8 rows per wave: 64 rows per block iteration, two table
+    groups) with an intermediate size that is a multiple of 32 but not of
+    64: the last iteration's second group lies past the output and must not
+    be written (a guard entry after the table stays untouched)."""
+    monkeypatch.setenv("WST_GEMV_RPW", "8")
+    in_f = 896
+    qw = wk.DeviceBuffer(2 * inter * in_f // 8, np.uint32)
+    si = wk.DeviceBuffer(2 * inter * in_f // 32, np.uint8)
+    sb = wk.DeviceBuffer(2 * inter, np.uint32)
+    ffi.call("wst_fixture_pack_hier", qw.ptr, si.ptr, sb.ptr, in_f, 0, 2 * inter, 0, 63, 0.02)
+    x = np.random.default_rng(inter).standard_normal(in_f).astype(np.float32)
+    xd = dev_f16(wk, f16(orc, x))
+    a1, a2 = wk.DeviceBuffer(inter, np.float16), wk.DeviceBuffer(inter, np.float16)
+    ffi.call("wst_gemv_hier_swiglu", qw.ptr, si.ptr, sb.ptr, xd.ptr, None, np.float32(1e-6),
+             a1.ptr, in_f, inter)
+    guard = np.full((inter // 32 + 1) * WORDS, 0xA5A5A5A5, np.uint32)
+    t2 = wk.DeviceBuffer.from_array(guard)
+    ffi.call("wst_gemv_hier_swiglu_xq", qw.ptr, si.ptr, sb.ptr, xd.ptr, None, np.float32(1e-6),
+             a2.ptr, t2.ptr, in_f, inter)
+    got = t2.numpy()
+    assert np.array_equal(a1.numpy().view(np.uint16), a2.numpy().view(np.uint16))
+    assert _same_entries(got[:inter // 32 * WORDS], _table(wk, a1, inter).numpy())
+    assert np.all(got[inter // 32 * WORDS:] == 0xA5A5A5A5)

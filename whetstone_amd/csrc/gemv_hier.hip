@@ -371,7 +371,8 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   if constexpr (XT) {
     // The DMA went out before the first units' loads (2 per group and row:
     // packed bytes and scale index); waiting for all but those many leaves
-    // the weights in flight. (The row scales may add more: a wait for less.)
+    // the weights in flight. (Where the compiler loads the row scales with
+    // vector loads too, the wait also covers the first of the weights.)
     asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * NR * NG * PD) : "memory");
   }
 #pragma unroll
@@ -500,12 +501,13 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       if (it % SUBS == SUBS - 1) {
         __syncthreads();
         const uint16_t *src = tws + ((it / SUBS) & 1) * RPB * SUBS;
-        const int nq = RPB * SUBS / 8;  // quads of 8 outputs: 4 per group
-        if (tid < nq) {
+        const int nq = RPB * SUBS / 8;  // threads of 8 outputs: 4 per group
+        const int r8 = row0(it - SUBS + 1) + 8 * tid;
+        if (tid < nq && r8 < nunits) {  // whole groups: nunits is a multiple of 32
           uint16_t h[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) h[e] = src[8 * tid + e];
-          build_xq(h, row0(it - SUBS + 1) / 8 + tid, true, tw);
+          build_xq(h, r8 / 8, true, tw);
         }
       }
     }
