@@ -73,16 +73,17 @@ struct AttnShape {
 // this many blocks per slice, each staging the same K/V tile, so that a slice's
 // score and P.V work is spread over more CUs. Every head's arithmetic is the
 // same in any group. Default: one group, or one block per head when the grid
-// would have fewer than 32 blocks (0.5B: 2 kv heads x 4 slices; attention 4.85
-// -> 4.4 us; on the 7B grid of 76 blocks two or more groups measured equal
-// or slower). WST_ATTN_HEAD_GROUPS overrides.
+// would have fewer than 64 blocks (0.5B: 2 kv heads x 4 slices, attention 4.85
+// -> 4.2 us; x 17 slices at a 4.3k cache, decode 1,440 -> 1,482 tok/s; on the
+// 7B grid of 76 blocks two or more groups measured equal or slower).
+// WST_ATTN_HEAD_GROUPS overrides.
 static int attn_head_groups(int gqa, int blocks) {
   static int v = -1;
   if (v < 0) {
     const char *e = getenv("WST_ATTN_HEAD_GROUPS");
     v = e ? atoi(e) : 0;
   }
-  int z = v > 0 ? v : (blocks < 32 ? gqa : 1);
+  int z = v > 0 ? v : (blocks < 64 ? gqa : 1);
   z = z < gqa ? z : gqa;
   const int hpz = (gqa + z - 1) / z;  // heads per group; every group gets >= 1
   return (gqa + hpz - 1) / hpz;
