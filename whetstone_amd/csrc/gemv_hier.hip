@@ -33,6 +33,10 @@
 //   depends only on (in_f, the row's bytes, x): not on the grid or on which
 //   fused form ran, so the fused kernels are checked bit for bit against the
 //   unfused ABI sequence.
+// * The table can come from the producer of x instead (XT: wst_gemv_hier_xq
+//   copies it memory -> LDS by DMA; TW: the SwiGLU form writes the table of
+//   its own output, taking its rows 32 at a time so a block holds every
+//   output of an entry). Both give the bits of the form that builds it.
 // * Rows wider than GEMV_MAX_G groups fall back to a simple kernel with the f16
 //   formulation (x read from L2).
 #include "common.hpp"
