@@ -605,16 +605,20 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
 }
 
 // sum over the splits of element i (stride `total`), in split order: the
-// loads are issued together (up to GM_MAXSPLIT), the adds stay in order.
+// loads are issued four at a time (a batch past the last split re-reads it),
+// the adds stay in order. A 4-way split costs 4 loads, not GM_MAXSPLIT.
 #define GM_MAXSPLIT 16
 __device__ __forceinline__ float split_sum(const float *__restrict__ ws, size_t i, size_t total,
                                            int splits) {
-  float v[GM_MAXSPLIT];
+  float t = 0.0f;
+  for (int z0 = 0; z0 < splits; z0 += 4) {
+    float v[4];
 #pragma unroll
-  for (int z = 0; z < GM_MAXSPLIT; ++z) v[z] = ws[(size_t)min(z, splits - 1) * total + i];
-  float t = v[0];
+    for (int e = 0; e < 4; ++e) v[e] = ws[(size_t)min(z0 + e, splits - 1) * total + i];
 #pragma unroll
-  for (int z = 1; z < GM_MAXSPLIT; ++z) t = z < splits ? t + v[z] : t;
+    for (int e = 0; e < 4; ++e)
+      if (z0 + e < splits) t = (z0 + e == 0) ? v[e] : t + v[e];
+  }
   return t;
 }
 
@@ -685,6 +689,49 @@ __global__ __launch_bounds__(64) void gemm_reduce_rope_kernel(
     return t;
   };
   const int pos = min(max(pos0 + tok, 0), max_seq - 1);
+  if (half <= 32) {
+    // One column per lane (lanes 0..31: the first half, 32..63: the second),
+    // the rotation partner over a cross-lane swap; the norm's sum and every
+    // product are those of the two-columns-per-lane form below.
+    const bool hi = j >= 32;
+    const int jj = j & 31;
+    const bool act = jj < half;
+    const int off = jj + (hi ? half : 0);
+    const float c = act ? cos_tab[(size_t)pos * half + jj] : 0.0f;
+    const float s = act ? sin_tab[(size_t)pos * half + jj] : 0.0f;
+    auto rotate = [&](float mine, const uint16_t *__restrict__ g, float &lo, float &hv) {
+      const float other = __shfl_xor(mine, 32);
+      float x1 = hi ? other : mine, x2 = hi ? mine : other;
+      if (g) {
+        const float ss = block_sum(act && !hi ? fmaf(x1, x1, x2 * x2) : 0.0f, red);
+        const float sc = 1.0f / sqrtf(ss / (float)hd + eps);
+        if (act) {
+          x1 = x1 * sc * h2f(g[jj]);
+          x2 = x2 * sc * h2f(g[jj + half]);
+        }
+      }
+      lo = rope_lo(x1, x2, c, s);
+      hv = rope_hi(x1, x2, c, s);
+    };
+    float lo, hv;
+    if (head < n_q) {
+      const int q0 = head * hd;
+      const float mine = act ? red_at(q0 + off) : 0.0f;
+      rotate(mine, q_norm_w, lo, hv);
+      if (act) row[q0 + off] = hi ? hv : lo;
+      return;
+    }
+    const int kvh = head - n_q;
+    const int k0 = (n_q + kvh) * hd, v0 = (n_q + n_kv + kvh) * hd;
+    const float km = act ? red_at(k0 + off) : 0.0f;
+    const float vm = act ? red_at(v0 + off) : 0.0f;
+    rotate(km, k_norm_w, lo, hv);
+    if (!act) return;
+    const size_t slot = ((size_t)kvh * max_seq + pos) * hd;
+    k_cache[slot + off] = f2h(hi ? hv : lo);
+    v_cache[slot + off] = f2h(vm);
+    return;
+  }
   const float c = active ? cos_tab[(size_t)pos * half + j] : 0.0f;
   const float s = active ? sin_tab[(size_t)pos * half + j] : 0.0f;
   if (head < n_q) {
