@@ -54,7 +54,9 @@ def test_gemm_swiglu_chunk_equals_gemm_then_swiglu(orc, wk, in_f, inter, n, exac
 @pytest.mark.parametrize("in_f,out_f,n,accum,bias", [(896, 896, 256, 1, False),
                                                      (4864, 896, 256, 1, False),
                                                      (3584, 3584, 37, 0, True),
-                                                     (96, 70, 5, 1, True)])
+                                                     (96, 70, 5, 1, True),
+                                                     (1536, 1536, 9, 1, True),
+                                                     (256, 4100, 3, 0, False)])
 def test_gemm_norm_chunk_equals_gemm_then_rmsnorm(orc, wk, in_f, out_f, n, accum, bias):
     lin = _lin(orc, wk, 31, in_f, out_f)
     x = _x(orc, wk, 32, n, in_f)

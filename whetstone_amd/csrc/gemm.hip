@@ -639,6 +639,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float *__r
 // (sum of the splits in split order) + bias, staged in LDS, then
 // h = f16(x * rms * w) with rms_scale512's order, so both outputs equal
 // gemm_split_reduce_kernel followed by rmsnorm_kernel bit for bit.
+template <int CPT>
 __global__ __launch_bounds__(512) void gemm_reduce_norm_kernel(
     const float *__restrict__ ws, const uint16_t *__restrict__ bias, float *__restrict__ y,
     int out_f, int n, int splits, int accum, const uint16_t *__restrict__ nw, float eps,
@@ -647,6 +648,37 @@ __global__ __launch_bounds__(512) void gemm_reduce_norm_kernel(
   extern __shared__ float xrow[];  // [out_f]: the reduced row
   const int tok = blockIdx.x;
   const size_t total = (size_t)n * out_f, base = (size_t)tok * out_f;
+  if constexpr (CPT > 0) {
+    // CPT columns per thread (out_f <= 512 * CPT): every global load (the
+    // splits, the bias, the residual, the norm weight) issued before the
+    // first wait, the columns past out_f clamped to the last one and not
+    // stored.
+    float t[CPT], w[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = min((int)threadIdx.x + 512 * k, out_f - 1);
+      w[k] = h2f(nw[c]);
+      float v = split_sum(ws, base + c, total, splits);
+      if (bias) v += h2f(bias[c]);
+      t[k] = accum ? y[base + c] + v : v;
+    }
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = threadIdx.x + 512 * k;
+      if (c < out_f) {
+        y[base + c] = t[k];
+        xrow[c] = t[k];
+      }
+    }
+    __syncthreads();
+    const float sc = rms_scale512(xrow, out_f, eps, red);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = threadIdx.x + 512 * k;
+      if (c < out_f) h[base + c] = f2h(t[k] * sc * w[k]);
+    }
+    return;
+  }
   // 1. the reduce, coalesced (thread t: elements t, t+512, ...)
   for (int c = threadIdx.x; c < out_f; c += 512) {
     float t = split_sum(ws, base + c, total, splits);
@@ -967,13 +999,17 @@ extern "C" wst_status_t wst_gemm_hier_norm_chunk(const void *qw, const void *si,
   if (st != WST_OK) return st;
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void *)gemm_reduce_norm_kernel,
+    (void)hipFuncSetAttribute((const void *)gemm_reduce_norm_kernel<0>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4);
     attr = true;
   }
-  gemm_reduce_norm_kernel<<<n, 512, (size_t)out_f * 4, WST_STREAM>>>(ws, (const uint16_t *)bias, (float *)y, out_f,
-                                                     n, splits, accum, (const uint16_t *)norm_w,
-                                                     eps, (uint16_t *)h_out);
+  auto kern = out_f <= 1024   ? gemm_reduce_norm_kernel<2>
+              : out_f <= 2048 ? gemm_reduce_norm_kernel<4>
+              : out_f <= 4096 ? gemm_reduce_norm_kernel<8>
+                              : gemm_reduce_norm_kernel<0>;
+  kern<<<n, 512, (size_t)out_f * 4, WST_STREAM>>>(ws, (const uint16_t *)bias, (float *)y, out_f, n,
+                                                  splits, accum, (const uint16_t *)norm_w, eps,
+                                                  (uint16_t *)h_out);
   WST_TRY_KERNEL("wst_gemm_hier_norm_chunk");
   return WST_OK;
 }
