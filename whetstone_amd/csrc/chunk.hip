@@ -170,7 +170,8 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   extern __shared__ __align__(16) uint16_t ac_lds[];
   const int head = blockIdx.x, t0 = blockIdx.y * AC_TT;
   const int kvh = head / (n_q / n_kv);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the tile loop is scalar
   const int r16 = lane & 15, kg = lane >> 4;
   uint16_t *vs = ac_lds + wave * S::WAVE_HALVES;  // V tile [AC_KT][VR], row-major
   uint16_t *ph = vs + AC_KT * S::VR;              // P hi [AC_KT][PR] ([pos][tok])
@@ -179,7 +180,10 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   const uint16_t *kb = k_cache + (size_t)kvh * max_seq * HD;
   const uint16_t *vb = v_cache + (size_t)kvh * max_seq * HD;
 
-  // q of token t0 + r16 as the A operand: dims 32s + 8kg + i, hi and lo parts.
+  // q of token t0 + r16 as the A operand: dims 32s + 8kg + i, hi and lo parts,
+  // scaled by log2(e) as well, so that the scores are in base 2 and the
+  // softmax exponentials are bare exp2.
+  const float qscale = scale * 1.44269504088896340736f;
   ac_h8 qh[S::KS], ql[S::KS];
   {
     const float *q = qkv + (size_t)min(t0 + r16, n - 1) * stride_row + (size_t)head * HD;
@@ -190,7 +194,7 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
       const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float x = v[i] * scale;
+        const float x = v[i] * qscale;
         const _Float16 h = (_Float16)x;
         qh[s][i] = h;
         ql[s][i] = (_Float16)(x - (float)h);
@@ -201,21 +205,27 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   const int kend = min(pos0 + tlast + 1, max_seq);  // positions [0, kend) are attended
   const int ntiles = (kend + AC_KT - 1) / AC_KT;
 
-  // Loads of key tile kt (positions clamped into [0, kend): unconditional loads
-  // stay batched): K in the B-operand layout, V rows as 16-byte pieces.
+  // Loads of key tile kt as buffer loads over [0, kend) of the head's cache
+  // rows: a lane's offset within a tile is fixed, the tile's is a scalar, and
+  // positions at or past kend read zeros (their scores are masked, their P is
+  // zero). K goes to the B-operand layout, V rows to 16-byte pieces.
+  const uint32_t kv_bytes = (uint32_t)kend * HD * 2u;
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void *)kb, 0, (int)kv_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void *)vb, 0, (int)kv_bytes, 0x00020000);
+  const uint32_t koff = (uint32_t)(r16 * HD + 8 * kg) * 2u;
+  const uint32_t voff = (uint32_t)((lane / (HD / 8)) * HD + 8 * (lane % (HD / 8))) * 2u;
 #define AC_LOAD_TILE(KR, VR_, KT)                                                           \
   do {                                                                                      \
-    const int p0_ = (KT) * AC_KT;                                                           \
-    _Pragma("unroll") for (int t2 = 0; t2 < 2; ++t2) {                                      \
-      const int p_ = min(p0_ + 16 * t2 + r16, kend - 1);                                    \
+    const int so_ = (KT) * (AC_KT * HD * 2);                                                \
+    _Pragma("unroll") for (int t2 = 0; t2 < 2; ++t2)                                        \
       _Pragma("unroll") for (int s = 0; s < S::KS; ++s) KR[t2][s] =                         \
-          *(const ac_u4 *)(kb + (size_t)p_ * HD + 32 * s + 8 * kg);                         \
-    }                                                                                       \
-    _Pragma("unroll") for (int j = 0; j < S::VU; ++j) {                                     \
-      const int u_ = lane + 64 * j;                                                         \
-      VR_[j] = *(const ac_u4 *)(vb + (size_t)min(p0_ + u_ / (HD / 8), kend - 1) * HD +      \
-                                8 * (u_ % (HD / 8)));                                       \
-    }                                                                                       \
+          __builtin_amdgcn_raw_buffer_load_b128(krs, koff + (16 * t2 * HD + 32 * s) * 2,    \
+                                                so_, 0);                                    \
+    _Pragma("unroll") for (int j = 0; j < S::VU; ++j) VR_[j] =                              \
+        __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + j * (64 / (HD / 8)) * HD * 2,     \
+                                              so_, 0);                                      \
   } while (0)
   ac_u4 kr[2][S::KS], vr[S::VU];
 
@@ -233,7 +243,7 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   AC_LOAD_TILE(kr, vr, min(kt, max(ntiles - 1, 0)));
   while (kt < ntiles) {
     const int p0 = kt * AC_KT;
-    // V tile into LDS (rows past kend hold duplicates; their P is zero)
+    // V tile into LDS (rows past kend hold zeros; their P is zero)
 #pragma unroll
     for (int j = 0; j < S::VU; ++j) {
       const int u = lane + 64 * j, pr = u / (HD / 8), ch = u % (HD / 8);
@@ -263,10 +273,11 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
     if (full) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float mx = dpp_max16(fmaxf(sc[0][i], sc[1][i]));
-        const float mn = fmaxf(m[i], mx);
-        corr[i] = (m[i] == -INFINITY) ? 0.0f : __expf(m[i] - mn);
-        const float pv0 = __expf(sc[0][i] - mn), pv1 = __expf(sc[1][i] - mn);
+        const float mx = dpp_max16(__builtin_elementwise_maximum(sc[0][i], sc[1][i]));
+        const float mn = __builtin_elementwise_maximum(m[i], mx);
+        corr[i] = (m[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[i] - mn);
+        const float pv0 = __builtin_amdgcn_exp2f(sc[0][i] - mn);
+        const float pv1 = __builtin_amdgcn_exp2f(sc[1][i] - mn);
         l[i] = l[i] * corr[i] + pv0 + pv1;  // this lane's columns; rows reduce at the end
         m[i] = mn;
         sc[0][i] = pv0;
@@ -282,12 +293,13 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
           const int p = p0 + 16 * t2 + r16;
           sv[t2] = (p <= lim && p < kend) ? sc[t2][i] : -INFINITY;
         }
-        const float mx = dpp_max16(fmaxf(sv[0], sv[1]));
-        const float mn = fmaxf(m[i], mx);
-        corr[i] = (m[i] == -INFINITY) ? 0.0f : __expf(m[i] - mn);
+        const float mx = dpp_max16(__builtin_elementwise_maximum(sv[0], sv[1]));
+        const float mn = __builtin_elementwise_maximum(m[i], mx);
+        corr[i] = (m[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[i] - mn);
         float pv[2];
 #pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) pv[t2] = (sv[t2] == -INFINITY) ? 0.0f : __expf(sv[t2] - mn);
+        for (int t2 = 0; t2 < 2; ++t2)
+          pv[t2] = (sv[t2] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sv[t2] - mn);
         l[i] = l[i] * corr[i] + pv[0] + pv[1];
         m[i] = mn;
         sc[0][i] = pv[0];
@@ -359,7 +371,7 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
 #pragma unroll
     for (int w = 0; w < AC_WAVES; ++w) {
       const float *wb = (const float *)(ac_lds + w * S::WAVE_HALVES) + row * (HD + 2);
-      const float f = (wb[0] == -INFINITY) ? 0.0f : __expf(wb[0] - M);
+      const float f = (wb[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(wb[0] - M);  // base 2
       num = fmaf(wb[2 + d], f, num);
       den = fmaf(wb[1], f, den);
     }

@@ -135,11 +135,16 @@ __device__ __forceinline__ float dpp_sum16(float v) {
   return v;
 }
 
+// The same four steps as fused DPP maxima, one VALU op each (written out:
+// the compiler's form is a DPP move, a canonicalising max and the max). Each
+// op reads the previous one's result through DPP, which needs two wait states
+// after the write: the s_nop 1 before each.
 __device__ __forceinline__ float dpp_max16(float v) {
-  v = fmaxf(v, dpp_f<0xB1>(v));
-  v = fmaxf(v, dpp_f<0x4E>(v));
-  v = fmaxf(v, dpp_f<0x141>(v));
-  v = fmaxf(v, dpp_f<0x140>(v));
+  asm("s_nop 1\n\tv_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\tv_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\tv_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\tv_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf"
+      : "+v"(v));
   return v;
 }
 
