@@ -121,8 +121,10 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
 //   softmax, and merge once at the end through LDS;
 // * scores S = q . k^T: q (already rotated, times 1/sqrt(hd)) enters as its f16
 //   hi part plus the f16 rounding of the rest, so the products keep ~22 bits;
-//   the K operand is loaded from the cache straight into registers in the
-//   MFMA B layout (16 bytes of one position per lane);
+//   K rows load coalesced (a 128-byte row per eight lanes) into LDS, and the
+//   B operand (16 bytes of one position per lane) is read from there: loaded
+//   straight into that layout, each load touched sixteen half rows and K's
+//   loads took about a quarter of the kernel;
 // * P . V: P (hi + lo, as q) and V are turned into MFMA operands with the
 //   gfx950 transposing LDS read (ds_read_b64_tr_b16): within 16 lanes, lane L's
 //   element i comes from lane 4i + L/4's element L%4, so V stays row-major in
@@ -146,9 +148,10 @@ struct AcShape {
   static constexpr int KS = HD / 32;              // k-steps of the scores
   static constexpr int NT = HD / 16;              // 16-dim output tiles
   static constexpr int VR = HD + 16;              // V row stride (halves)
+  static constexpr int KR = HD + 8;               // K row stride (halves)
   static constexpr int PR = AC_TT;                // P row stride (halves): [pos][tok]
   static constexpr int VU = AC_KT * HD / 8 / 64;  // 16-byte V pieces per lane per tile
-  static constexpr int WAVE_HALVES = AC_KT * VR + 2 * AC_KT * PR;
+  static constexpr int WAVE_HALVES = AC_KT * VR + AC_KT * KR + 2 * AC_KT * PR;
   static constexpr int LDS = AC_WAVES * WAVE_HALVES * 2;
   static_assert(16 * (HD + 2) * 4 <= WAVE_HALVES * 2, "the merge rows fit a wave's region");
 };
@@ -176,6 +179,7 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   uint16_t *vs = ac_lds + wave * S::WAVE_HALVES;  // V tile [AC_KT][VR], row-major
   uint16_t *ph = vs + AC_KT * S::VR;              // P hi [AC_KT][PR] ([pos][tok])
   uint16_t *pl = ph + AC_KT * S::PR;              // P lo
+  uint16_t *ks = pl + AC_KT * S::PR;              // K tile [AC_KT][KR], row-major
   const int stride_row = (n_q + 2 * n_kv) * HD;
   const uint16_t *kb = k_cache + (size_t)kvh * max_seq * HD;
   const uint16_t *vb = v_cache + (size_t)kvh * max_seq * HD;
@@ -208,26 +212,25 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   // Loads of key tile kt as buffer loads over [0, kend) of the head's cache
   // rows: a lane's offset within a tile is fixed, the tile's is a scalar, and
   // positions at or past kend read zeros (their scores are masked, their P is
-  // zero). K goes to the B-operand layout, V rows to 16-byte pieces.
+  // zero). K and V rows both load as 16-byte pieces, eight lanes to a
+  // 128-byte row, and go through LDS.
   const uint32_t kv_bytes = (uint32_t)kend * HD * 2u;
   const __amdgpu_buffer_rsrc_t krs =
       __builtin_amdgcn_make_buffer_rsrc((void *)kb, 0, (int)kv_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void *)vb, 0, (int)kv_bytes, 0x00020000);
-  const uint32_t koff = (uint32_t)(r16 * HD + 8 * kg) * 2u;
   const uint32_t voff = (uint32_t)((lane / (HD / 8)) * HD + 8 * (lane % (HD / 8))) * 2u;
-#define AC_LOAD_TILE(KR, VR_, KT)                                                           \
+#define AC_LOAD_TILE(KR_, VR_, KT)                                                          \
   do {                                                                                      \
     const int so_ = (KT) * (AC_KT * HD * 2);                                                \
-    _Pragma("unroll") for (int t2 = 0; t2 < 2; ++t2)                                        \
-      _Pragma("unroll") for (int s = 0; s < S::KS; ++s) KR[t2][s] =                         \
-          __builtin_amdgcn_raw_buffer_load_b128(krs, koff + (16 * t2 * HD + 32 * s) * 2,    \
-                                                so_, 0);                                    \
+    _Pragma("unroll") for (int j = 0; j < S::VU; ++j) KR_[j] =                              \
+        __builtin_amdgcn_raw_buffer_load_b128(krs, voff + j * (64 / (HD / 8)) * HD * 2,     \
+                                              so_, 0);                                      \
     _Pragma("unroll") for (int j = 0; j < S::VU; ++j) VR_[j] =                              \
         __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + j * (64 / (HD / 8)) * HD * 2,     \
                                               so_, 0);                                      \
   } while (0)
-  ac_u4 kr[2][S::KS], vr[S::VU];
+  ac_u4 kr[S::VU], vr[S::VU];
 
   float m[4], l[4];
   ac_f4 o[S::NT];
@@ -243,10 +246,11 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   AC_LOAD_TILE(kr, vr, min(kt, max(ntiles - 1, 0)));
   while (kt < ntiles) {
     const int p0 = kt * AC_KT;
-    // V tile into LDS (rows past kend hold zeros; their P is zero)
+    // K and V tiles into LDS (rows past kend hold zeros; their P is zero)
 #pragma unroll
     for (int j = 0; j < S::VU; ++j) {
       const int u = lane + 64 * j, pr = u / (HD / 8), ch = u % (HD / 8);
+      *(ac_u4 *)(ks + pr * S::KR + 8 * ch) = kr[j];
       *(ac_u4 *)(vs + pr * S::VR + 8 * ch) = vr[j];
     }
     // scores for positions p0 + 16 t2 + r16, tokens 4kg + i
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
       ac_f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < S::KS; ++s) {
-        const ac_h8 b = __builtin_bit_cast(ac_h8, kr[t2][s]);
+        const ac_h8 b = *(const ac_h8 *)(ks + (16 * t2 + r16) * S::KR + 32 * s + 8 * kg);
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], b, c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[s], b, c, 0, 0, 0);
       }
