@@ -828,6 +828,17 @@ struct GemmPlan {
   dim3 grid;
 };
 
+// WST_GEMM_SPLITS=k caps the split-K count at k (1: no split); a measurement
+// knob.
+static int gemm_split_cap() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("WST_GEMM_SPLITS");
+    v = e ? atoi(e) : 0;
+  }
+  return v;
+}
+
 static int gemm_bn_override() {
   static int v = -1;
   if (v < 0) {
@@ -868,7 +879,8 @@ GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0, b
   p.gps = G;
   const int target = wst_cu_count();
   if (tiles < target / 2) {
-    const int want = (target + tiles - 1) / tiles;
+    int want = (target + tiles - 1) / tiles;
+    if (gemm_split_cap() > 0) want = min(want, gemm_split_cap());
     int g = (G + want - 1) / want;
     g = (g + p.kg - 1) / p.kg * p.kg;
     if ((G + g - 1) / g > GM_MAXSPLIT) g = (G + GM_MAXSPLIT - 1) / GM_MAXSPLIT;
