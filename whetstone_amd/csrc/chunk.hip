@@ -215,6 +215,8 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   // zero). K and V rows both load as 16-byte pieces, eight lanes to a
   // 128-byte row, and go through LDS.
   const uint32_t kv_bytes = (uint32_t)kend * HD * 2u;
+  // 0x00020000: word 3 of a raw gfx9 buffer resource (32-bit data format,
+  // no swizzle); a load past kv_bytes returns zeros.
   const __amdgpu_buffer_rsrc_t krs =
       __builtin_amdgcn_make_buffer_rsrc((void *)kb, 0, (int)kv_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs =
@@ -408,6 +410,9 @@ extern "C" wst_status_t wst_attn_chunk(const void *qkv, const void *k_cache, con
               "wst_attn_chunk: chunk does not fit the cache");
   WST_REQUIRE(!(((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u),
               "wst_attn_chunk: qkv and the caches must be 16-byte aligned");
+  // The MFMA kernel addresses a head's cache rows with 32-bit buffer offsets.
+  WST_REQUIRE((int64_t)max_seq * head_dim * 2 < ((int64_t)1 << 31),
+              "wst_attn_chunk: a head's cache rows exceed 2 GiB");
   const dim3 grid(n_q, n);
   switch (head_dim) {
     case 64:
