@@ -119,12 +119,12 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
 // * one 512-thread block per (query head, 16 query tokens); its eight waves
 //   take key tiles of 32 positions round-robin, each with its own online
 //   softmax, and merge once at the end through LDS;
-// * scores S = q . k^T: q (already rotated, times 1/sqrt(hd)) enters as its f16
-//   hi part plus the f16 rounding of the rest, so the products keep ~22 bits;
-//   K rows load coalesced (a 128-byte row per eight lanes) into LDS, and the
-//   B operand (16 bytes of one position per lane) is read from there: loaded
-//   straight into that layout, each load touched sixteen half rows and K's
-//   loads took about a quarter of the kernel;
+// * scores S = q . k^T: q (already rotated, times log2(e)/sqrt(hd), so the
+//   softmax is in base 2) enters as its f16 hi part plus the f16 rounding of
+//   the rest, so the products keep ~22 bits; K rows load coalesced (a
+//   128-byte row per eight lanes) into LDS, and the B operand (16 bytes of one
+//   position per lane) is read from there (loaded straight into that layout,
+//   each load touched sixteen part rows: hd 128 was 13% slower);
 // * P . V: P (hi + lo, as q) and V are turned into MFMA operands with the
 //   gfx950 transposing LDS read (ds_read_b64_tr_b16): within 16 lanes, lane L's
 //   element i comes from lane 4i + L/4's element L%4, so V stays row-major in
