@@ -18,6 +18,16 @@ The line printed carries:
              dequant + forward) on the same weights and context, timed on the
              host cores for a bounded number of tokens
   cpu_check  the GPU's first-step logits and tokens against that CPU run
+  secondary  (config 3 without --no-secondary) the other GPU configurations,
+             each measured once after the headline's timed region: config 2
+             (0.5B decode, 512-token prefill, 256 steps), config 4 (4096-token
+             chunked prefill with counted TFLOP/s, then 128 decode steps),
+             config 1 (the 0.5B lm_head GEMV, weights cold)
+  config.full_range_tok_s  (config 3, when --steps is not 256) the whole
+             2048 -> 2304 range, timed after the headline's steps
+
+The config-3 KV cache always holds the configuration's 2304 positions (+8), so
+attention's grid is the configuration's whatever --steps is.
 
     python bench.py [--steps 256] [--warmup 8] [--config 3|2] [--cpu-seconds 12]
 
@@ -45,6 +55,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "batch=1 decode tok/s + achieved HBM GB/s (% of 8 TB/s), Qwen2.5-0.5B/7B int4"
 HBM_PEAK_GBS = 8000.0
 KV_SEED, WEIGHT_SEED, PROMPT_SEED = 2, 0, 1
+FULL_RANGE = 256  # config 3 decodes context 2048 -> 2304
 TIMED_STAGES = ["qkv", "attn", "o", "gate_up", "down", "head"]
 KERNEL_NAMES = {  # kernels each stage launches in the fused step (rocprof names)
     "qkv": "gemv_hier_kernel<NG, WPR, XB, 512, NORM=true, SWIGLU=false, PD>",
@@ -71,6 +82,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline budget (tokens are added until it is spent)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-secondary", action="store_true",
+                   help="with --config 3: skip the configs 1, 2 and 4 measured after the "
+                        "headline's timed region")
     p.add_argument("--stage-reps", type=int, default=20)
     p.add_argument("--max-seq", type=int, default=0,
                    help="KV-cache capacity for configs 2 and 3 (default: the context plus the "
@@ -297,7 +311,8 @@ def chunk_gemm_times(wk, shapes, n: int = 256, reps: int = 50) -> dict:
     return out
 
 
-def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False) -> None:
+def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False, gemms: bool = True,
+                  emit: bool = True) -> dict:
     """Config 4: chunked prefill of 4096 tokens (256 per chunk), then n_new
     graph decode steps (none, and no graph capture, for n_new = 0)."""
     cfg = dict(E.QWEN05B, qk_norm=1, rescore_k=32)
@@ -344,7 +359,7 @@ def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False) -> None:
         shapes.update({"7b gate_up+swiglu": ("swiglu", H7, 2 * I7), "7b down": ("gemm", I7, H7),
                        "7b qkv": ("gemm", H7, (c7["n_q"] + 2 * c7["n_kv"]) * c7["head_dim"]),
                        "7b o": ("gemm", c7["n_q"] * c7["head_dim"], H7)})
-    gemms = chunk_gemm_times(wk, shapes, chunk)
+    gemms = chunk_gemm_times(wk, shapes, chunk) if gemms else None
     line = {
         "metric": "chunked prefill tok/s (config 4)", "value": round(n_prompt / dt_p, 1),
         "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "dtype": "int4xf16->f32",
@@ -362,7 +377,69 @@ def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False) -> None:
     }
     eng.close()
     g.close()
-    print(json.dumps(line), flush=True)
+    if emit:
+        print(json.dumps(line), flush=True)
+    return line
+
+
+def decode_05b(E, wk, n_prompt: int = 512, n_new: int = 256, warmup: int = 8) -> dict:
+    """Config 2: the 0.5B shape, a seeded n_prompt-token chunked prefill, then
+    n_new graph steps (one replay and a 4-byte token read-back each)."""
+    cfg = E.QWEN05B
+    g = E.Model(cfg, seed=WEIGHT_SEED)
+    eng = E.Engine(g, n_prompt + n_new + 8)
+    prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt)
+    eng.prefill(prompt.astype(np.int32), chunked=True)
+    eng.capture_graph()
+    tok0 = eng.token()
+    for _ in range(warmup):
+        eng.step()
+        eng.token()
+    eng.set_pos(n_prompt)
+    eng.set_token(tok0)
+    wk.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n_new):
+        eng.step()
+        eng.token()
+    wk.synchronize()
+    dt = time.perf_counter() - t0
+    bts = []
+    for i in range(n_new):
+        eng.set_pos(n_prompt + i)
+        bts.append(eng.step_bytes())
+    eng.close()
+    g.close()
+    b = float(np.mean(bts))
+    tok_s = n_new / dt
+    return {"workload": f"config 2: 0.5B-shape decode, {n_prompt}-token chunked prefill, "
+                        f"context {n_prompt} -> {n_prompt + n_new}, captured graph",
+            "tok_s": round(tok_s, 1), "ms_per_token": round(dt / n_new * 1e3, 4),
+            "bytes_per_token": int(b), "hbm_gbs": round(b * tok_s / 1e9, 1),
+            "frac_of_hbm_peak": round(b * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+            "token_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / b, 1)}
+
+
+def secondary_configs(E, wk) -> dict:
+    """Configs 2, 4 and 1 at their own workloads, each measured once after the
+    headline's timed region (nothing here is inside it)."""
+    out = {}
+    log("secondary: config 2 (0.5B decode after a 512-token prefill, 256 steps)")
+    out["config2"] = decode_05b(E, wk)
+    log("secondary: config 4 (4096-token chunked prefill, then 128 decode steps)")
+    p = prefill_bench(E, wk, 128, gemms=False, emit=False)
+    c = p["config"]
+    out["config4"] = {"workload": c["workload"], "prefill_tok_s": p["value"],
+                      "prefill_ms": c["prefill_ms"], "prefill_tflops": c["prefill_tflops"],
+                      "decode_tok_s": c["decode_tok_s"]}
+    log("secondary: config 1 (lm_head GEMV 896 -> 151936, weights cold)")
+    h = gemv_bench(wk, 200, head_only=True, emit=False)["config"]["shapes"]["lm_head"]
+    out["config1"] = {"workload": "config 1: int4-hier GEMV 896 -> 151936, weights cold past "
+                                  "the MALL", "us_per_call": h["cold"]["us_per_call"],
+                      "gbs": h["cold"]["gbs"], "frac_of_hbm_peak": h["cold"]["frac"],
+                      "stream_read_floor_us": h["stream_read_floor_cold"]["us_per_call"],
+                      "gemv_frac_of_floor": h["gemv_frac_of_floor"]}
+    return out
 
 
 def floors_bench(E, wk, config: int, reps: int) -> None:
@@ -519,7 +596,7 @@ def cpu_reference_bench(E, wk) -> None:
     print(json.dumps(line), flush=True)
 
 
-def gemv_bench(wk, reps: int) -> None:
+def gemv_bench(wk, reps: int, head_only: bool = False, emit: bool = True) -> dict:
     """Config 1: the int4-hier-g32 GEMV alone, y f32 = W x (x f16 N(0,1), W
     N(0,0.02) packed on the device), on the 0.5B lm_head shape and the 0.5B
     block shapes. "cold" cycles through ceil(512 MB / matrix bytes) distinct
@@ -529,6 +606,8 @@ def gemv_bench(wk, reps: int) -> None:
     from whetstone_amd import ffi
     shapes = [("lm_head", 896, 151936), ("qkv", 896, 1152), ("gate_up", 896, 9728),
               ("down", 4864, 896)]
+    if head_only:
+        shapes = shapes[:1]
     res = {}
     for name, in_f, out_f in shapes:
         wbytes = out_f * (in_f // 2 + in_f // 32 + 4)
@@ -598,7 +677,9 @@ def gemv_bench(wk, reps: int) -> None:
                      "unit": "GB/s", "frac": head["frac"],
                      "traffic": traffic_for(1, "lm_head", GEMV_TRAFFIC_FILE)},
     }
-    print(json.dumps(line), flush=True)
+    if emit:
+        print(json.dumps(line), flush=True)
+    return line
 
 
 def main():
@@ -639,7 +720,9 @@ def main():
     ms_need = None
     if a.config == 3:
         ctx0 = 2048
-        ms_need = ctx0 + max(a.steps, a.warmup) + 8
+        # the configuration's cache: context 2048 -> 2304 (the reference CLI's
+        # max(ctx, prompt + max_new + 1), run.rs:103), or longer for more steps
+        ms_need = ctx0 + max(a.steps, a.warmup, FULL_RANGE) + 8
         eng = E.Engine(g, max(a.max_seq, ms_need))
         eng.fill_kv(KV_SEED, ctx0)
         workload = ("config 3: Qwen2.5-7B-shape int4 hier-g32 batch=1 greedy decode, "
@@ -680,6 +763,18 @@ def main():
         eng.set_pos(ctx0 + i)
         bytes_steps.append(eng.step_bytes())
     bytes_tok = float(np.mean(bytes_steps))
+    full = None
+    if a.config == 3 and a.steps != FULL_RANGE:
+        # the configuration's whole range, 2048 -> 2304, outside the timed region
+        eng.set_pos(ctx0)
+        eng.set_token(tok0)
+        wk.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(FULL_RANGE):
+            eng.step()
+            eng.token()
+        wk.synchronize()
+        full = round(FULL_RANGE / (time.perf_counter() - t1), 2)
 
     log(f"{a.steps / dt:.1f} tok/s; timing each stage kernel")
     # Per-kernel timing at the middle of the timed context range.
@@ -723,6 +818,8 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
     }
+    if full is not None:
+        line["config"]["full_range_tok_s"] = full
     if a.no_cpu:
         line["cpu_baseline"] = None
     else:
@@ -733,6 +830,8 @@ def main():
         line["cpu_check"] = check
     eng.close()
     g.close()
+    if a.config == 3 and not a.no_secondary:
+        line["secondary"] = secondary_configs(E, wk)
     print(json.dumps(line), flush=True)
 
 

@@ -184,6 +184,314 @@ void orc_xq14(const uint16_t *x, int64_t n, double *out) {
   }
 }
 
+/* ------------------------------------------- ORC_ACC_REF: the reference's own
+ * arithmetic on its CUDA build (acc = ORC_ACC_REF)
+ *
+ * Every reduction in the order and precision the reference's kernels compute
+ * it, on a device with `g_ref_sms` multiprocessors (the attention split count
+ * depends on it, attention.cu:201-218; default 30, the fallback the reference
+ * itself uses and the RTX 2060 its README quotes):
+ *
+ *   int4 GEMV   gemv_hier.cu:91-163, hier.cuh:24-60: lane l of a 32-lane warp
+ *               takes groups l, l+32, ...; per group an f16 x-sum (`__hadd2`:
+ *               even and odd columns in two f16 lanes, 16 steps each, one RNE
+ *               rounding per step), an f16 dot (`__hfma2` of (q-8) and x, 16
+ *               steps per half, ONE rounding per step), both halves widened and
+ *               added in f32, then fmaf(s, dot, acc), fmaf(fmaf(8,s,m), sx, acc);
+ *               the lanes' partials summed by the xor butterfly (a halving tree)
+ *   fp16 GEMV   gemv_int4.cu:194-229: lane l takes half2 pairs l, l+32, ...,
+ *               two fmaf per pair, butterfly
+ *   RMSNorm     decode.cu:46-100: n <= 1024: one element per thread of
+ *               ceil(n/32)*32, x*x; else 256 threads, fmaf over i = t, t+256..;
+ *               block_reduce_sum (common.cuh:149-161: butterfly per warp, warp
+ *               sums through warp 0's butterfly); f16(x*inv*w)
+ *   QK-norm     common.cuh:185-202: fmaf(x1,x1,x2*x2) per lane, block sum
+ *   RoPE        decode.cu:150-174: x1*c - x2*s and x2*c + x1*s as nvcc
+ *               contracts them (LLVM fuses the left product of an fsub/fadd:
+ *               fmaf(x1,c,-(x2*s)), fmaf(x2,c,x1*s)) -- an assumption, nvcc's
+ *               default -fmad=true leaves the form to the compiler
+ *   attention   attention.cu:57-193: splits per pick_splits, 8 warps per split
+ *               block, warp w takes positions t0+w, t0+w+8, ..., score by a
+ *               per-lane fmaf chain over d = lane+32i and the butterfly, online
+ *               softmax per warp, the block's warps merged in order, then the
+ *               splits merged in order
+ *   SwiGLU      decode.cu:240-242: f16((g * (1/(1+exp(-g)))) * u)
+ *   rescore     head_rescore.cu:272-281: 256 threads, fmaf, block sum
+ *   embedding   gemv_hier.cu:186: q*(d*ls) - dm*lm, contracted to
+ *               fmaf(q, d*ls, -(dm*lm))
+ *
+ * Not restated: the reference's `__expf` and `rsqrtf` are hardware
+ * approximations (a few ulp); ref_exp (f64 exp rounded to f32) and 1/sqrtf
+ * stand in for them. Their
+ * difference is a relative 1e-7-scale perturbation of single values, far below
+ * the f16 roundings above. */
+#define HGROUP 32
+static int g_ref_sms = 30;
+
+void orc_set_ref_sms(int sms) { g_ref_sms = sms > 0 ? sms : 30; }
+
+/* exp for the REF mode: the f64 exponential rounded to f32 (correctly rounded
+ * but for ties closer than 2^-29 relative), standing in for __expf. */
+static inline float ref_exp(float x) { return (float)exp((double)x); }
+
+/* IEEE binary16 round-to-nearest-even of a double (exact for the values the
+ * f16 arithmetic below produces: multiples of 2^-24 far inside double's range). */
+uint16_t orc_d2h(double v) {
+  uint64_t b;
+  memcpy(&b, &v, 8);
+  const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+  const int ex = (int)((b >> 52) & 0x7FF);
+  const uint64_t man = b & ((1ull << 52) - 1);
+  if (ex == 0x7FF) return man ? (uint16_t)(sign | 0x7E00u) : (uint16_t)(sign | 0x7C00u);
+  if (ex == 0) return sign; /* double subnormals are far below f16's half-ulp */
+  const int e = ex - 1023;
+  if (e > 15) return (uint16_t)(sign | 0x7C00u);
+  const uint64_t m = man | (1ull << 52); /* value = m * 2^(e-52) */
+  /* f16 quantum: 2^(e-10) for normals, 2^-24 below 2^-14 */
+  const int qexp = (e >= -14 ? e : -14) - 10;
+  const int shift = qexp - (e - 52); /* bits of m below the quantum */
+  if (shift > 60) return sign;
+  const uint64_t q = m >> shift, rem = m & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+  uint64_t r = q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
+  /* r is the magnitude in units of 2^qexp; f16 bits = biased exponent field
+   * of the quantum's binade plus r, carry into the exponent included */
+  uint32_t bits;
+  if (qexp == -24) {
+    bits = (uint32_t)r; /* subnormal (r == 1024 is the smallest normal) */
+  } else {
+    /* r in [1024, 2048]: (biased exponent e + 15) << 10 | (r - 1024) */
+    bits = ((uint32_t)(e + 14) << 10) + (uint32_t)r;
+  }
+  if (bits >= 0x7C00u) return (uint16_t)(sign | 0x7C00u);
+  return (uint16_t)(sign | bits);
+}
+
+/* __hadd / __hfma on one f16 lane: the exact result (every product and sum of
+ * these f16 values is exact in double) rounded once. */
+uint16_t orc_ref_hadd(uint16_t a, uint16_t b) {
+  return orc_d2h((double)h2f(a) + (double)h2f(b));
+}
+uint16_t orc_ref_hfma(uint16_t a, uint16_t b, uint16_t c) {
+  return orc_d2h((double)h2f(a) * (double)h2f(b) + (double)h2f(c));
+}
+
+/* The xor butterfly of warp_reduce_sum (common.cuh:127-132) as lane 0 sees it:
+ * p[i] += p[i + off] for off = 16, 8, 4, 2, 1. */
+static float ref_warp_sum(float *p) {
+  for (int off = 16; off >= 1; off >>= 1)
+    for (int i = 0; i < off; ++i) p[i] += p[i + off];
+  return p[0];
+}
+
+/* block_reduce_sum (common.cuh:149-161) over `nthreads` per-thread values. */
+static float ref_block_sum(const float *v, int nthreads) {
+  const int nwarps = (nthreads + 31) / 32;
+  float ws[32];
+  for (int w = 0; w < nwarps; ++w) {
+    float p[32];
+    for (int l = 0; l < 32; ++l) p[l] = (w * 32 + l < nthreads) ? v[w * 32 + l] : 0.0f;
+    ws[w] = ref_warp_sum(p);
+  }
+  float p[32];
+  for (int l = 0; l < 32; ++l) p[l] = l < nwarps ? ws[l] : 0.0f;
+  return ref_warp_sum(p);
+}
+
+/* f16 RNE of n * 2^-24 for an integer n (every f16 value, and every exact
+ * sum or (q-8)*x product of them, is such a multiple); the result again in
+ * units of 2^-24. *ovf is set when the f16 result would be infinite. */
+static inline int64_t rnd16_units(int64_t n, int *ovf) {
+  const uint64_t a = (uint64_t)(n < 0 ? -n : n);
+  if (a < 2048u) return n; /* subnormals and the lowest binade: exact */
+  const int sh = 53 - __builtin_clzll(a); /* bit length - 11 */
+  const uint64_t q = a >> sh, rem = a & ((1ull << sh) - 1), half = 1ull << (sh - 1);
+  const uint64_t r = (q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0)) << sh;
+  if (r >= (65520ull << 24)) *ovf = 1;
+  return n < 0 ? -(int64_t)r : (int64_t)r;
+}
+
+/* The same row arithmetic as ref_gemv_row below on integer f16 images
+ * (X[c] = x[c] * 2^24). A group's f16 x-sum and f16 dot do not depend on the
+ * lane that computes them, so the x-sums (sx[g], shared by every row) and the
+ * row's dots are formed first, four groups at a time for instruction-level
+ * parallelism, then each lane folds its groups in the kernel's order. Returns 0
+ * if an f16 partial overflowed. */
+static void ref_xsums_units(const int64_t *X, int64_t groups, float *sx, int *ovf) {
+  const float u = 0x1p-24f;
+  for (int64_t v = 0; v < groups; ++v) {
+    const int64_t *xg = X + v * HGROUP;
+    int64_t xs0 = 0, xs1 = 0;
+    for (int i = 0; i < 16; ++i) {
+      xs0 = rnd16_units(xs0 + xg[2 * i], ovf);
+      xs1 = rnd16_units(xs1 + xg[2 * i + 1], ovf);
+    }
+    sx[v] = (float)xs0 * u + (float)xs1 * u;
+  }
+}
+
+static int ref_gemv_row_units(const uint32_t *qr, const uint8_t *sr, uint32_t sbw,
+                              const int64_t *X, const float *sx, int64_t groups,
+                              float *dot, float *out) {
+  const float d = h2f((uint16_t)(sbw & 0xFFFFu));
+  const float dm = h2f((uint16_t)(sbw >> 16));
+  const float u = 0x1p-24f;
+  int ovf = 0;
+  for (int64_t v0 = 0; v0 < groups; v0 += 4) {
+    const int nv = groups - v0 < 4 ? (int)(groups - v0) : 4;
+    int64_t acc[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+    for (int w = 0; w < 4; ++w)
+      for (int i = 0; i < 4; ++i)
+        for (int k = 0; k < nv; ++k) {
+          const int64_t v = v0 + k;
+          const uint32_t word = qr[v * 4 + w];
+          const int64_t *xg = X + v * HGROUP;
+          const int64_t q0 = (int64_t)((word >> (8 * i)) & 0xFu) - 8;
+          const int64_t q1 = (int64_t)((word >> (8 * i + 4)) & 0xFu) - 8;
+          acc[k][0] = rnd16_units(q0 * xg[8 * w + 2 * i] + acc[k][0], &ovf);
+          acc[k][1] = rnd16_units(q1 * xg[8 * w + 2 * i + 1] + acc[k][1], &ovf);
+        }
+    for (int k = 0; k < nv; ++k) dot[v0 + k] = (float)acc[k][0] * u + (float)acc[k][1] * u;
+  }
+  if (ovf) return 0;
+  float lanes[32];
+  for (int lane = 0; lane < 32; ++lane) {
+    float a = 0.0f;
+    for (int64_t v = lane; v < groups; v += 32) {
+      const uint8_t idx = sr[v];
+      const float s = d * (float)(idx & 0xF);
+      const float m = -dm * (float)(idx >> 4);
+      a = fmaf(s, dot[v], a);
+      a = fmaf(fmaf(8.0f, s, m), sx[v], a);
+    }
+    lanes[lane] = a;
+  }
+  *out = ref_warp_sum(lanes);
+  return 1;
+}
+
+/* One row of gemv_int4_hier_kernel (gemv_hier.cu:118-163), lane partials
+ * folded by the butterfly; x given as f16 bits. */
+static float ref_gemv_row(const uint32_t *qr, const uint8_t *sr, uint32_t sbw,
+                          const uint16_t *x, int64_t groups) {
+  const float d = h2f((uint16_t)(sbw & 0xFFFFu));
+  const float dm = h2f((uint16_t)(sbw >> 16));
+  float acc[32];
+  for (int lane = 0; lane < 32; ++lane) {
+    float a = 0.0f;
+    for (int64_t v = lane; v < groups; v += 32) {
+      const uint16_t *xg = x + v * HGROUP;
+      uint16_t xs0 = 0, xs1 = 0;
+      for (int i = 0; i < 16; ++i) {
+        xs0 = orc_ref_hadd(xs0, xg[2 * i]);
+        xs1 = orc_ref_hadd(xs1, xg[2 * i + 1]);
+      }
+      const float sx = h2f(xs0) + h2f(xs1);
+      const uint8_t idx = sr[v];
+      const float s = d * (float)(idx & 0xF);
+      const float m = -dm * (float)(idx >> 4);
+      uint16_t d0 = 0, d1 = 0;
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t word = qr[v * 4 + w];
+        for (int i = 0; i < 4; ++i) {
+          const double q0 = (double)((word >> (8 * i)) & 0xFu) - 8.0;
+          const double q1 = (double)((word >> (8 * i + 4)) & 0xFu) - 8.0;
+          d0 = orc_d2h(q0 * (double)h2f(xg[8 * w + 2 * i]) + (double)h2f(d0));
+          d1 = orc_d2h(q1 * (double)h2f(xg[8 * w + 2 * i + 1]) + (double)h2f(d1));
+        }
+      }
+      const float dotf = h2f(d0) + h2f(d1);
+      a = fmaf(s, dotf, a);
+      a = fmaf(fmaf(8.0f, s, m), sx, a);
+    }
+    acc[lane] = a;
+  }
+  return ref_warp_sum(acc);
+}
+
+/* attention.cu:201-218: slices per head such that 2 blocks per SM are busy,
+ * at most 16, none thinner than the 8 warps of a split block. */
+int orc_ref_attn_splits(int n_q, int max_seq) {
+  int splits = (2 * g_ref_sms + n_q - 1) / n_q;
+  if (splits < 1) splits = 1;
+  if (splits > 16) splits = 16;
+  while (splits > 1 && max_seq / splits < 8) splits--;
+  return splits;
+}
+
+/* attention.cu:57-193 as the reference computes it (see the ORC_ACC_REF note). */
+static void ref_attn_decode(const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                            uint16_t *out, int n_q, int gqa, int hd, int seq, int max_seq,
+                            float scale) {
+  const int splits = orc_ref_attn_splits(n_q, max_seq);
+  const int epl = hd / 32, per = (seq + splits - 1) / splits;
+  float *part = (float *)malloc((size_t)splits * (hd + 2) * sizeof(float));
+  for (int h = 0; h < n_q; ++h) {
+    const int kvh = h / gqa;
+    const uint16_t *kb = k_cache + (size_t)kvh * max_seq * hd;
+    const uint16_t *vb = v_cache + (size_t)kvh * max_seq * hd;
+    float qs[1024];
+    for (int i = 0; i < hd; ++i) qs[i] = q[(size_t)h * hd + i] * scale;
+    for (int sp = 0; sp < splits; ++sp) {
+      float *o = part + (size_t)sp * (hd + 2);
+      const int t0 = sp * per, t1 = t0 + per < seq ? t0 + per : seq;
+      if (t0 >= t1) {
+        o[0] = -INFINITY;
+        o[1] = 0.0f;
+        for (int i = 0; i < hd; ++i) o[2 + i] = 0.0f;
+        continue;
+      }
+      float m_s[8], l_s[8], acc_s[8][1024];
+      for (int w = 0; w < 8; ++w) {
+        float m = -INFINITY, l = 0.0f;
+        for (int i = 0; i < hd; ++i) acc_s[w][i] = 0.0f;
+        for (int t = t0 + w; t < t1; t += 8) {
+          const uint16_t *kt = kb + (size_t)t * hd, *vt = vb + (size_t)t * hd;
+          float p[32];
+          for (int lane = 0; lane < 32; ++lane) {
+            float a = 0.0f;
+            for (int i = 0; i < epl; ++i) a = fmaf(qs[lane + 32 * i], h2f(kt[lane + 32 * i]), a);
+            p[lane] = a;
+          }
+          const float sc = ref_warp_sum(p);
+          const float m_new = fmaxf(m, sc);
+          const float corr = ref_exp(m - m_new);
+          const float pr = ref_exp(sc - m_new);
+          for (int d = 0; d < hd; ++d) acc_s[w][d] = fmaf(pr, h2f(vt[d]), acc_s[w][d] * corr);
+          l = fmaf(l, corr, pr);
+          m = m_new;
+        }
+        m_s[w] = m;
+        l_s[w] = l;
+      }
+      float M = -INFINITY;
+      for (int w = 0; w < 8; ++w) M = fmaxf(M, m_s[w]);
+      for (int d = 0; d < hd; ++d) {
+        float num = 0.0f;
+        for (int w = 0; w < 8; ++w) num = fmaf(acc_s[w][d], ref_exp(m_s[w] - M), num);
+        o[2 + d] = num;
+      }
+      float den = 0.0f;
+      for (int w = 0; w < 8; ++w) den = fmaf(l_s[w], ref_exp(m_s[w] - M), den);
+      o[0] = M;
+      o[1] = den;
+    }
+    /* attn_merge_kernel, attention.cu:172-193 */
+    float M = -INFINITY;
+    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, part[(size_t)sp * (hd + 2)]);
+    for (int d = 0; d < hd; ++d) {
+      float num = 0.0f, den = 0.0f;
+      for (int sp = 0; sp < splits; ++sp) {
+        const float *pp = part + (size_t)sp * (hd + 2);
+        const float f = ref_exp(pp[0] - M);
+        num = fmaf(pp[2 + d], f, num);
+        den = fmaf(pp[1], f, den);
+      }
+      out[(size_t)h * hd + d] = f2h(num / den);
+    }
+  }
+  free(part);
+}
+
 /* ---------------------------------------------------- fixture generator */
 
 /* splitmix64 (Steele, Lea, Flood 2014): the published finaliser. */
@@ -219,7 +527,6 @@ void orc_fixture_normal_n(uint64_t seed, uint64_t stream, uint64_t index0, float
 
 /* ------------------------------------------------------ int4-hier-g32 */
 
-#define HGROUP 32
 #define QMAX 15.0f
 #define SMAX 15.0f
 
@@ -420,6 +727,35 @@ void orc_dequantize_int4_hier(const uint32_t *qw, const uint8_t *si, const uint3
 void orc_gemv_int4_hier(const uint32_t *qw, const uint8_t *si, const uint32_t *sb,
                         const uint16_t *x, const uint16_t *bias, float *y, int64_t in_f,
                         int64_t out_f, int accum) {
+  if (g_acc == ORC_ACC_REF) {
+    const int64_t groups = in_f / HGROUP;
+    int64_t *X = (int64_t *)malloc((size_t)in_f * sizeof(int64_t));
+    float *sx = (float *)malloc((size_t)groups * sizeof(float));
+    int finite = 1, ovf = 0;
+    for (int64_t c = 0; c < in_f; ++c) {
+      finite &= (x[c] & 0x7C00u) != 0x7C00u;
+      X[c] = finite ? (int64_t)ldexp((double)h2f(x[c]), 24) : 0;
+    }
+    if (finite) ref_xsums_units(X, groups, sx, &ovf);
+    const int fast = finite && !ovf;
+#pragma omp parallel
+    {
+      float *dot = (float *)malloc((size_t)groups * sizeof(float));
+#pragma omp for schedule(static)
+      for (int64_t r = 0; r < out_f; ++r) {
+        float rr;
+        if (!fast ||
+            !ref_gemv_row_units(qw + r * (in_f / 8), si + r * groups, sb[r], X, sx, groups, dot, &rr))
+          rr = ref_gemv_row(qw + r * (in_f / 8), si + r * groups, sb[r], x, groups);
+        if (bias) rr += h2f(bias[r]);
+        y[r] = accum ? y[r] + rr : rr;
+      }
+      free(dot);
+    }
+    free(X);
+    free(sx);
+    return;
+  }
   double *xd = (double *)malloc((size_t)in_f * sizeof(double));
   if (g_xq)
     orc_xq14(x, in_f, xd);
@@ -454,6 +790,25 @@ void orc_gemv_int4_hier(const uint32_t *qw, const uint8_t *si, const uint32_t *s
 /* gemv_int4.cu:194-229 (fp16 weights), same epilogue. */
 void orc_gemv_fp16(const uint16_t *w, const uint16_t *x, const uint16_t *bias, float *y,
                    int64_t in_f, int64_t out_f, int accum) {
+  if (g_acc == ORC_ACC_REF) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < out_f; ++r) {
+      const uint16_t *wr = w + r * in_f;
+      float p[32];
+      for (int lane = 0; lane < 32; ++lane) {
+        float a = 0.0f;
+        for (int64_t c = lane; c < in_f / 2; c += 32) {
+          a = fmaf(h2f(wr[2 * c]), h2f(x[2 * c]), a);
+          a = fmaf(h2f(wr[2 * c + 1]), h2f(x[2 * c + 1]), a);
+        }
+        p[lane] = a;
+      }
+      float rr = ref_warp_sum(p);
+      if (bias) rr += h2f(bias[r]);
+      y[r] = accum ? y[r] + rr : rr;
+    }
+    return;
+  }
 #pragma omp parallel
   {
     float *t = (float *)malloc((size_t)in_f * sizeof(float));
@@ -478,6 +833,20 @@ void orc_gemv_fp16(const uint16_t *w, const uint16_t *x, const uint16_t *bias, f
 
 /* decode.cu:46-82: out = f16(x * rsqrt(mean(x^2) + eps) * w). */
 void orc_rmsnorm(const float *x, const uint16_t *w, uint16_t *out, int n, float eps) {
+  if (g_acc == ORC_ACC_REF) {
+    const int T = n <= 1024 ? (n + 31) / 32 * 32 : 256;
+    float *t = (float *)calloc((size_t)T, sizeof(float));
+    if (n <= 1024) {
+      for (int i = 0; i < n; ++i) t[i] = x[i] * x[i];
+    } else {
+      for (int th = 0; th < T; ++th)
+        for (int i = th; i < n; i += T) t[th] = fmaf(x[i], x[i], t[th]);
+    }
+    const float inv = 1.0f / sqrtf(ref_block_sum(t, T) / (float)n + eps);
+    for (int i = 0; i < n; ++i) out[i] = f2h(x[i] * inv * h2f(w[i]));
+    free(t);
+    return;
+  }
   if (g_acc != ORC_ACC_F64) {
     float *t = (float *)malloc((size_t)n * sizeof(float));
     for (int i = 0; i < n; ++i) t[i] = x[i] * x[i];
@@ -531,6 +900,43 @@ void orc_rope_cache(float *qkv, uint16_t *k_cache, uint16_t *v_cache, const floa
   if (pos > max_seq - 1) pos = max_seq - 1;
   const float *c = cos_tab + (size_t)pos * half;
   const float *s = sin_tab + (size_t)pos * half;
+  if (g_acc == ORC_ACC_REF) {
+    const int T = (half + 31) / 32 * 32;
+    for (int h = 0; h < n_q + n_kv; ++h) {
+      float *src = qkv + (size_t)h * hd;
+      float x1[512], x2[512], t[544];
+      for (int j = 0; j < half; ++j) {
+        x1[j] = src[j];
+        x2[j] = src[j + half];
+      }
+      const uint16_t *g = h < n_q ? q_norm_w : k_norm_w;
+      if (g) {
+        for (int j = 0; j < T; ++j) t[j] = j < half ? fmaf(x1[j], x1[j], x2[j] * x2[j]) : 0.0f;
+        const float inv = 1.0f / sqrtf(ref_block_sum(t, T) / (float)hd + eps);
+        for (int j = 0; j < half; ++j) {
+          x1[j] = x1[j] * inv * h2f(g[j]);
+          x2[j] = x2[j] * inv * h2f(g[j + half]);
+        }
+      }
+      float r[1024];
+      for (int j = 0; j < half; ++j) {
+        r[j] = fmaf(x1[j], c[j], -(x2[j] * s[j]));
+        r[j + half] = fmaf(x2[j], c[j], x1[j] * s[j]);
+      }
+      if (h < n_q) {
+        for (int i = 0; i < hd; ++i) src[i] = r[i];
+      } else {
+        const int kvh = h - n_q;
+        const size_t slot = ((size_t)kvh * max_seq + pos) * hd;
+        const float *vv = qkv + (size_t)(n_q + n_kv + kvh) * hd;
+        for (int i = 0; i < hd; ++i) {
+          k_cache[slot + i] = f2h(r[i]);
+          v_cache[slot + i] = f2h(vv[i]);
+        }
+      }
+    }
+    return;
+  }
   double v[1024];
   for (int h = 0; h < n_q + n_kv; ++h) {
     float *src = qkv + (size_t)h * hd;
@@ -564,6 +970,10 @@ void orc_attn_decode(const float *q, const uint16_t *k_cache, const uint16_t *v_
   int seq = (pos < 0 ? 0 : pos) + 1;
   if (seq > max_seq) seq = max_seq;
   const int gqa = n_q / n_kv;
+  if (g_acc == ORC_ACC_REF) {
+    ref_attn_decode(q, k_cache, v_cache, out, n_q, gqa, hd, seq, max_seq, scale);
+    return;
+  }
   if (g_acc != ORC_ACC_F64) {
     float *e = (float *)malloc((size_t)seq * sizeof(float));
     float *t = (float *)malloc((size_t)(seq > hd ? seq : hd) * sizeof(float));
@@ -626,6 +1036,13 @@ void orc_attn_decode(const float *q, const uint16_t *k_cache, const uint16_t *v_
 
 /* decode.cu:235-242: out = f16(g * sigmoid(g) * u), g = first half. */
 void orc_swiglu(const float *gate_up, uint16_t *out, int n) {
+  if (g_acc == ORC_ACC_REF) {
+    for (int i = 0; i < n; ++i) {
+      const float g = gate_up[i];
+      out[i] = f2h(g * (1.0f / (1.0f + ref_exp(-g))) * gate_up[i + n]);
+    }
+    return;
+  }
   for (int i = 0; i < n; ++i) {
     const double g = gate_up[i], u = gate_up[i + n];
     out[i] = f2h((float)(g / (1.0 + exp(-g)) * u));
@@ -684,6 +1101,16 @@ void orc_head_rescore(const uint16_t *head, const uint16_t *x, float *logits, in
                       int hidden, float thresh) {
   for (int r = 0; r < n; ++r) {
     if (logits[r] < thresh) continue;
+    if (g_acc == ORC_ACC_REF) {
+      float t[256];
+      for (int th = 0; th < 256; ++th) {
+        t[th] = 0.0f;
+        for (int i = th; i < hidden; i += 256)
+          t[th] = fmaf(h2f(head[(size_t)r * hidden + i]), h2f(x[i]), t[th]);
+      }
+      logits[r] = ref_block_sum(t, 256);
+      continue;
+    }
     double acc = 0.0;
     for (int i = 0; i < hidden; ++i)
       acc += (double)h2f(head[(size_t)r * hidden + i]) * (double)h2f(x[i]);
@@ -718,6 +1145,20 @@ struct orc_model {
   uint16_t *embed16, *head16;
   layer_t *layers;
 };
+
+/* embed_int4_hier_kernel (gemv_hier.cu:168-189): q*(d*ls) - dm*lm, as nvcc
+ * contracts it (ORC_ACC_REF only; the default keeps hier.rs's two roundings). */
+static void ref_embed_row(const hmat_t *e, int64_t row, float *dst) {
+  const int64_t in_f = e->in_f, groups = in_f / HGROUP, words = in_f / 8;
+  const uint32_t sbw = e->sb[row];
+  const float d = h2f((uint16_t)(sbw & 0xFFFFu));
+  const float dm = h2f((uint16_t)(sbw >> 16));
+  for (int64_t c = 0; c < in_f; ++c) {
+    const float q = (float)((e->qw[row * words + c / 8] >> (4 * (c % 8))) & 0xFu);
+    const uint8_t idx = e->si[row * groups + c / HGROUP];
+    dst[c] = fmaf(q, d * (float)(idx & 0xF), -(dm * (float)(idx >> 4)));
+  }
+}
 
 /* Fixture streams: one per (layer, tensor); the GPU generator uses the same. */
 enum { ST_Q = 0, ST_K = 1, ST_V = 2, ST_O = 3, ST_GATE = 4, ST_UP = 5, ST_DOWN = 6,
@@ -1051,6 +1492,8 @@ int32_t orc_step(orc_state_t *s, int32_t token, float *logits_out) {
     uint16_t *act = (uint16_t *)malloc((size_t)I * 2);
     if (m->embed16) {  /* decode.cu:259-268: the f16 row widened to f32 */
       for (int i = 0; i < H; ++i) x[i] = h2f(m->embed16[(size_t)token * H + i]);
+    } else if (g_acc == ORC_ACC_REF) {
+      ref_embed_row(&m->embed, token, x);
     } else {
       orc_dequantize_row(m->embed.qw, m->embed.si, m->embed.sb, H, token, x);
     }

@@ -57,6 +57,18 @@ void orc_dequantize_row(const uint32_t *qw, const uint8_t *si, const uint32_t *s
 #define ORC_ACC_F64 0
 #define ORC_ACC_F32_SEQ 1
 #define ORC_ACC_F32_LANE 2
+/* ORC_ACC_REF: every reduction in the order and precision of the reference's
+ * CUDA kernels (f16 __hfma2/__hadd2 group sums in the int4 GEMV, 32-lane
+ * butterflies, block reductions, per-warp online softmax and the split merge),
+ * on a device of orc_set_ref_sms() multiprocessors (default 30). */
+#define ORC_ACC_REF 3
+void orc_set_ref_sms(int sms);
+/* Splits per head of the reference's attention at that SM count. */
+int orc_ref_attn_splits(int n_q, int max_seq);
+/* IEEE binary16 RNE of a double; one f16 lane of __hadd2 / __hfma2. */
+uint16_t orc_d2h(double v);
+uint16_t orc_ref_hadd(uint16_t a, uint16_t b);
+uint16_t orc_ref_hfma(uint16_t a, uint16_t b, uint16_t c);
 void orc_set_variant(int acc, int xq);
 /* The activation table's value of each f16 activation (groups of 32). */
 void orc_xq14(const uint16_t *x, int64_t n, double *out);

@@ -98,6 +98,11 @@ def lib():
         "orc_threads": (C.c_int, []),
         "orc_set_variant": (None, [C.c_int, C.c_int]),
         "orc_xq14": (None, [_u16p, C.c_int64, _f64p]),
+        "orc_set_ref_sms": (None, [C.c_int]),
+        "orc_ref_attn_splits": (C.c_int, [C.c_int, C.c_int]),
+        "orc_d2h": (C.c_uint16, [C.c_double]),
+        "orc_ref_hadd": (C.c_uint16, [C.c_uint16, C.c_uint16]),
+        "orc_ref_hfma": (C.c_uint16, [C.c_uint16, C.c_uint16, C.c_uint16]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -312,13 +317,14 @@ class State:
         return int(nxt), logits
 
 
-ACC_F64, ACC_F32_SEQ, ACC_F32_LANE = 0, 1, 2
+ACC_F64, ACC_F32_SEQ, ACC_F32_LANE, ACC_REF = 0, 1, 2, 3
 
 
 class variant:
     """Context manager for the oracle's arithmetic variants (process-wide):
     `acc` picks how reductions are summed (ACC_F64 default, or f32 in
-    ascending order / as 64 lane partials and a tree), `xq` rounds int4-GEMV
+    ascending order / as 64 lane partials and a tree, or ACC_REF: the
+    reference CUDA kernels' own f16 group sums and reduction orders), `xq` rounds int4-GEMV
     activations to the GPU activation table's 14-bit per-group fixed point."""
 
     def __init__(self, acc: int = ACC_F64, xq: bool = False):

@@ -16,6 +16,13 @@ told from a bug. No reference code is imported or run.
         and the oracle's two f32 summation orders (first-step logits and
         their 64-token streams). About 4 minutes to pack on 8 threads, 4 s per
         token.
+  7bref adds to qwen7b_ctx2048_greedy.json the oracle's ORC_ACC_REF forward
+        (the reference CUDA kernels' own arithmetic: f16 group sums in the
+        GEMV, their reduction orders, attention split for a 30-SM device):
+        its first-step logits at the same sample, its full-vector distance
+        from the f64-summing oracle, and its 64-token stream with margins;
+        the first step also at 132 SMs (another split count). About 15
+        minutes on 8 threads.
   cfg2  qwen05b_ctx512_greedy.json: config 2's workload, the 0.5B shape with a
         seeded 512-token prompt and 256 greedy tokens (context 512 -> 768),
         plus the first generated step's logits under the oracle's two f32
@@ -120,6 +127,54 @@ def golden_7b():
                     mirrored_vs_f32_lane=float(np.max(np.abs(lg0 - drift["f32_lane"]))))), t0)
 
 
+def golden_7b_ref():
+    t0 = time.time()
+    path = HERE / "qwen7b_ctx2048_greedy.json"
+    g = json.loads(path.read_text())
+    ctx, cfg = g["context"], O.QWEN7B
+    m = O.Model(cfg, g["seed"])
+    print(f"7b packed in {time.time() - t0:.0f}s", flush=True)
+
+    def state():
+        st = O.State(m, ctx + N_NEW + 8, 0)
+        st.fill_kv(g["kv_seed"], ctx)
+        st.pos = ctx
+        return st
+
+    st = state()
+    f64 = st.step(g["first_token"])[1].astype(np.float64)
+    st.close()
+    idx = np.asarray(g["first_step_logits"]["index"])
+    assert np.array_equal(f64[idx].astype(np.float32),
+                          np.asarray(g["first_step_logits"]["value"], np.float32))
+    lib = O.lib()
+    lib.orc_set_ref_sms(132)
+    with O.variant(O.ACC_REF):
+        st = state()
+        ref132 = st.step(g["first_token"])[1].astype(np.float64)
+        st.close()
+    lib.orc_set_ref_sms(30)
+    with O.variant(O.ACC_REF):
+        st = state()
+        nxt, lg = st.step(g["first_token"])
+        ref = lg.astype(np.float64)
+        print(f"7b ref first step {time.time() - t0:.0f}s: vs f64 {np.max(np.abs(ref - f64)):.4f}",
+              flush=True)
+        tokens, margins, top = _decode(st, nxt, lg, N_NEW)
+        st.close()
+    g["ref"] = dict(
+        sms=30,
+        first_step_sample=[float(ref[i]) for i in idx],
+        first_step_vs_f64=float(np.max(np.abs(ref - f64))),
+        first_step_allclose_1e3_1e2=bool(np.allclose(ref, f64, rtol=1e-3, atol=1e-2)),
+        first_step_vs_f64_at_132_sms=float(np.max(np.abs(ref132 - f64))),
+        first_step_30_vs_132_sms=float(np.max(np.abs(ref - ref132))),
+        tokens=tokens, margins=margins, top_logit=top,
+        seconds=round(time.time() - t0, 1))
+    path.write_text(json.dumps(g, indent=1))
+    print(f"wrote {path} in {time.time() - t0:.1f}s", flush=True)
+
+
 def golden_cfg2():
     t0 = time.time()
     cfg = O.QWEN05B
@@ -170,4 +225,5 @@ def golden_cfg4():
 if __name__ == "__main__":
     which = sys.argv[1:] or ["05b"]
     for w in which:
-        {"05b": golden_05b, "7b": golden_7b, "cfg2": golden_cfg2, "cfg4": golden_cfg4}[w]()
+        {"05b": golden_05b, "7b": golden_7b, "7bref": golden_7b_ref, "cfg2": golden_cfg2,
+         "cfg4": golden_cfg4}[w]()

@@ -523,3 +523,42 @@ def test_chunk_attention_equals_per_token_decode_attention(orc, wk, n_q, n_kv, h
         q = np.ascontiguousarray(qkv[j * row:j * row + n_q * hd])
         orc.lib().orc_attn_decode(q, kc, vc, want, n_q, n_kv, hd, pos0 + j, max_seq, scale)
         assert np.max(np.abs(got[j] - orc.f16_value(want))) < 2e-3, j
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,pos0,n,max_seq", [
+    (14, 2, 64, 0, 256, 300), (28, 4, 128, 1000, 44, 1100), (14, 2, 64, 45, 256, 301),
+    (28, 4, 128, 7, 20, 61)])
+def test_chunk_attention_ignores_nonfinite_past_the_attended_end(orc, wk, n_q, n_kv, hd, pos0,
+                                                                n, max_seq):
+    """Cache positions at or past the chunk's last attended position hold NaN
+    and Inf (inside the allocation): the output stays finite and equal to
+    decode attention, so no tile reads them (a read would give 0 * NaN = NaN
+    in P.V). Capacities that are not a multiple of the 32-position tile put
+    the last tile past the allocation's end as well."""
+    rng = np.random.default_rng(pos0 + n + max_seq)
+    kend = min(pos0 + n, max_seq)
+    kc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
+    vc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
+    bad = np.where(np.arange((max_seq - kend) * hd) % 2 == 0, 0x7E00, 0x7C00).astype(np.uint16)
+    for c in (kc, vc):
+        c3 = c.reshape(n_kv, max_seq, hd)
+        c3[:, kend:, :] = bad.reshape(max_seq - kend, hd)
+    row = (n_q + 2 * n_kv) * hd
+    qkv = (rng.standard_normal(n * row) * 2).astype(np.float32)
+    cache = wk.KvCache(n_kv, n_q, hd, max_seq)
+    cache.k.copy_from(kc.view(np.float16))
+    cache.v.copy_from(vc.view(np.float16))
+    qd = wk.DeviceBuffer.from_array(qkv)
+    out = wk.DeviceBuffer(n * n_q * hd, np.float16)
+    scale = np.float32(1.0 / math.sqrt(hd))
+    print(f"chunk attention with NaN/Inf past position {kend}: n_q {n_q} hd {hd} pos0 {pos0} "
+          f"n {n} max_seq {max_seq}", flush=True)
+    ffi.call("wst_attn_chunk", qd.ptr, cache.k.ptr, cache.v.ptr, out.ptr, n_q, n_kv, hd, pos0, n,
+             max_seq, scale)
+    got = out.numpy().astype(np.float64).reshape(n, n_q * hd)
+    assert np.all(np.isfinite(got))
+    for j in range(n):
+        want = np.empty(n_q * hd, np.uint16)
+        q = np.ascontiguousarray(qkv[j * row:j * row + n_q * hd])
+        orc.lib().orc_attn_decode(q, kc, vc, want, n_q, n_kv, hd, pos0 + j, max_seq, scale)
+        assert np.max(np.abs(got[j] - orc.f16_value(want))) < 2e-3, j

@@ -210,10 +210,12 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   const int ntiles = (kend + AC_KT - 1) / AC_KT;
 
   // Loads of key tile kt as buffer loads over [0, kend) of the head's cache
-  // rows: a lane's offset within a tile is fixed, the tile's is a scalar, and
-  // positions at or past kend read zeros (their scores are masked, their P is
-  // zero). K and V rows both load as 16-byte pieces, eight lanes to a
-  // 128-byte row, and go through LDS.
+  // rows. The whole byte offset (the lane's within the tile plus the tile's)
+  // goes in the vector offset, which is the offset the buffer range check
+  // compares with num_records, so positions at or past kend read zeros
+  // whatever the cache holds there (their scores are masked, their P is zero),
+  // and no load reaches past the allocation. K and V rows both load as
+  // 16-byte pieces, eight lanes to a 128-byte row, and go through LDS.
   const uint32_t kv_bytes = (uint32_t)kend * HD * 2u;
   // 0x00020000: word 3 of a raw gfx9 buffer resource (32-bit data format,
   // no swizzle); a load past kv_bytes returns zeros.
@@ -224,13 +226,13 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   const uint32_t voff = (uint32_t)((lane / (HD / 8)) * HD + 8 * (lane % (HD / 8))) * 2u;
 #define AC_LOAD_TILE(KR_, VR_, KT)                                                          \
   do {                                                                                      \
-    const int so_ = (KT) * (AC_KT * HD * 2);                                                \
+    const uint32_t so_ = (uint32_t)(KT) * (AC_KT * HD * 2);                                \
     _Pragma("unroll") for (int j = 0; j < S::VU; ++j) KR_[j] =                              \
-        __builtin_amdgcn_raw_buffer_load_b128(krs, voff + j * (64 / (HD / 8)) * HD * 2,     \
-                                              so_, 0);                                      \
+        __builtin_amdgcn_raw_buffer_load_b128(krs, so_ + voff + j * (64 / (HD / 8)) * HD * 2, \
+                                              0, 0);                                        \
     _Pragma("unroll") for (int j = 0; j < S::VU; ++j) VR_[j] =                              \
-        __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + j * (64 / (HD / 8)) * HD * 2,     \
-                                              so_, 0);                                      \
+        __builtin_amdgcn_raw_buffer_load_b128(vrs, so_ + voff + j * (64 / (HD / 8)) * HD * 2, \
+                                              0, 0);                                        \
   } while (0)
   ac_u4 kr[S::VU], vr[S::VU];
 
