@@ -28,6 +28,10 @@
 //   about 4.7 us; the separate merge about 3.
 // * The grid covers max_seq; only the ceil(seq/P) slices holding cached
 //   positions do work, so a captured graph serves every position.
+// * A slice is one tile of P positions by default. WST_ATTN_TILES makes it
+//   several, looped with an online softmax (measured: with at most 8 slices
+//   the o GEMV can merge them and the merge launch goes, but on the 7B cache
+//   the tile loop and the larger merge in o cost more than the launch saves).
 // * ROPE form (wst_attn_decode_fused): each block applies QK-norm and RoPE to
 //   the q heads it needs exactly as wst_rope_cache does (same per-head
 //   reduction, same fma shapes) while its K/V loads are in flight; the block
@@ -64,8 +68,8 @@ struct AttnShape {
   static constexpr int S_OFF = QL_OFF + 16 * QS * 2;   // scores [16][P] f32
   static constexpr int PH_OFF = S_OFF + 16 * P * 4;
   static constexpr int PL_OFF = PH_OFF + 16 * PS * 2;
-  static constexpr int ML_OFF = PL_OFF + 16 * PS * 2;  // per head (m, l)
-  static constexpr int LDS = ML_OFF + 16 * 2 * 4;
+  static constexpr int ML_OFF = PL_OFF + 16 * PS * 2;  // per head (m, l, rescale)
+  static constexpr int LDS = ML_OFF + 16 * 3 * 4;
   static_assert(P % 32 == 0 && HD % 32 == 0, "MFMA tiles");
 };
 
@@ -89,23 +93,45 @@ static int attn_head_groups(int gqa, int blocks) {
   return (gqa + hpz - 1) / hpz;
 }
 
-// Slices are 16384 / hd positions (128 at hd 128): measured on the 7B shape
-// at 2k context (4 kv heads), 32- and 64-position slices launch 4-2x the
+// Tiles are 16384 / hd positions (128 at hd 128): measured on the 7B shape
+// at 2k context (4 kv heads), 32- and 64-position tiles launch 4-2x the
 // blocks but run slower (slice kernel 6.8 us at 32 against 5.6 us at 128;
 // step 754 / 779 / 774 tok/s at 32 / 64 / 128), since every block pays the
 // same chain of dependent phases. WST_ATTN_SLICE=<positions> (32, 64, 128 or
 // 256, within 16384 / hd and at least 64 threads) overrides, for measurement.
-int wst_attn_slice_len(int hd, int max_seq) {
+static int attn_tile_len(int hd) {
   static int forced = -1;
   if (forced < 0) {
     const char *e = getenv("WST_ATTN_SLICE");
     forced = e ? atoi(e) : 0;
   }
   const int pmax = 16384 / hd;
-  (void)max_seq;
   if (forced == 32 || forced == 64 || forced == 128 || forced == 256)
     if (forced <= pmax && forced * hd >= 2048) return forced;
   return pmax;
+}
+
+// Tiles per slice (1 to 4, the default tile length only). WST_ATTN_TILES=n
+// forces n; WST_ATTN_TILES=auto takes the fewest that leave at most 8 slices
+// (AM_MAX_SLICES: the o GEMV can then merge them itself).
+static int attn_tiles(int hd, int max_seq) {
+  static int forced = -1;
+  if (forced < 0) {
+    const char *e = getenv("WST_ATTN_TILES");
+    forced = !e ? 1 : (e[0] == 'a' ? 0 : atoi(e));
+    if (forced < 0 || forced > 4) forced = 1;
+  }
+  const int P = attn_tile_len(hd);
+  if (P != 16384 / hd || hd > 128) return 1;
+  if (forced > 0) return forced;
+  const int ntiles = (max_seq + P - 1) / P;
+  const int t = (ntiles + 7) / 8;
+  return t < 1 ? 1 : (t > 4 ? 4 : t);
+}
+
+// Positions per slice: the tile length times the tiles per slice.
+int wst_attn_slice_len(int hd, int max_seq) {
+  return attn_tile_len(hd) * attn_tiles(hd, max_seq);
 }
 
 static inline int attn_slices(int head_dim, int max_seq) {
@@ -152,13 +178,22 @@ __device__ __forceinline__ void store_q(uint16_t *qh, uint16_t *ql, int at, floa
   ql[at] = f2h(v - h2f(h));
 }
 
-template <int HD, int P_, bool ROPE>
+// NTL: tiles of P positions per slice. A slice of NTL * P positions is
+// processed tile by tile with an online softmax: per head the running (m, l)
+// live in LDS, the P.V accumulators in the MFMA result registers, each rescaled
+// by exp(m_old - m_new) before the next tile's products are added; the next
+// tile's K/V loads are issued as soon as the current one is in LDS. With
+// NTL = 1 the arithmetic is that of a single tile (the rescale of a zero
+// accumulator by zero adds nothing).
+template <int HD, int P_, bool ROPE, int NTL>
 __global__ __launch_bounds__(P_ * HD / 32) void attn_decode_kernel(
     const float *__restrict__ qkv, uint16_t *__restrict__ k_cache,
     uint16_t *__restrict__ v_cache, float *__restrict__ partials, int n_q, int n_kv,
     const int32_t *__restrict__ pos_dev, int max_seq, float scale, RopeArgs ra) {
   using S = AttnShape<HD, P_>;
   constexpr int P = S::P, CH = S::CH, T = S::T, NW = S::NW;
+  constexpr int SP = P * NTL;  // positions per slice
+  constexpr int ND = (HD / 16 + NW - 1) / NW;  // 16-dim output tiles per wave
   (void)CH;
   extern __shared__ __align__(16) unsigned char lds[];
   uint16_t *ktile = (uint16_t *)(lds + S::K_OFF);
@@ -168,7 +203,7 @@ __global__ __launch_bounds__(P_ * HD / 32) void attn_decode_kernel(
   float *sc = (float *)(lds + S::S_OFF);
   uint16_t *ph = (uint16_t *)(lds + S::PH_OFF);
   uint16_t *pl = (uint16_t *)(lds + S::PL_OFF);
-  float *ml = (float *)(lds + S::ML_OFF);
+  float *ml = (float *)(lds + S::ML_OFF);  // per head: m, l, and the tile's rescale
 
   const int gqa = n_q / n_kv;
   const int kvh = blockIdx.x, split = blockIdx.y, nsplit = gridDim.y;
@@ -181,29 +216,32 @@ __global__ __launch_bounds__(P_ * HD / 32) void attn_decode_kernel(
 
   const int pos = min(max(*pos_dev, 0), max_seq - 1);
   const int seq = min(max(*pos_dev, 0) + 1, max_seq);
-  const int nactive = (seq + P - 1) / P;
+  const int nactive = (seq + SP - 1) / SP;
   if (split >= nactive) return;  // no cached positions here (uniform per block)
-  const int t0 = split * P, t1 = min(t0 + P, seq);
+  const int t0 = split * SP, tend = min(t0 + SP, seq);
 
   const uint16_t *kb = k_cache + (size_t)kvh * max_seq * HD;
   const uint16_t *vb = v_cache + (size_t)kvh * max_seq * HD;
 
-  // ---- phase A: the slice's K and V requests go out first, all at once.
+  // ---- phase A: the first tile's K and V requests go out first, all at once.
   // Thread t holds 16-byte chunk ch = t % CH (dims 8ch..8ch+7) of the four
-  // consecutive positions 4 (t / CH) + i.
+  // consecutive positions 4 (t / CH) + i of a tile.
   constexpr int LD = P * CH / T;
   static_assert(LD == 4, "four positions per thread");
   const int lch = tid % CH, lrow = 4 * (tid / CH);
   uint4 kr[LD], vr[LD];
+  auto load_tile = [&](int tt0) {
 #pragma unroll
-  for (int i = 0; i < LD; ++i) {
-    const int t = min(t0 + lrow + i, seq - 1);  // clamped: unconditional loads stay batched
-    kr[i] = *(const uint4 *)(kb + (size_t)t * HD + lch * 8);
-    vr[i] = *(const uint4 *)(vb + (size_t)t * HD + lch * 8);
-  }
+    for (int i = 0; i < LD; ++i) {
+      const int t = min(tt0 + lrow + i, seq - 1);  // clamped: unconditional loads stay batched
+      kr[i] = *(const uint4 *)(kb + (size_t)t * HD + lch * 8);
+      vr[i] = *(const uint4 *)(vb + (size_t)t * HD + lch * 8);
+    }
+  };
+  load_tile(t0);
 
   // q for the group's heads, pre-scaled (attention.cu:98-101), into LDS.
-  const bool owner = ROPE && pos >= t0 && pos < t1;
+  const bool owner = ROPE && pos >= t0 && pos < tend;  // the slice holds `pos`
   uint16_t knew = 0, vnew = 0, knew2 = 0, vnew2 = 0;  // owner: this position's k, v
   if constexpr (ROPE) {
     // One wave per head, as wst_rope_cache runs one 64-thread block per head
@@ -264,125 +302,172 @@ __global__ __launch_bounds__(P_ * HD / 32) void attn_decode_kernel(
       if (e < nqv) store_q(qh, ql, (e / HD) * S::QS + e % HD, qv[i] * scale);
     }
   }
+  if (tid < hb) {
+    ml[tid * 3] = -INFINITY;
+    ml[tid * 3 + 1] = 0.0f;
+  }
 
-  // Tiles into LDS; rows past the cached positions are zero (their scores are
-  // masked, and a zero V row keeps 0 * v finite).
-  uint32_t vw[LD][4];
+  f32x4 oc[ND];
 #pragma unroll
-  for (int i = 0; i < LD; ++i) {
-    const uint32_t mk = t0 + lrow + i < t1 ? 0xFFFFFFFFu : 0u;  // a mask, not a select of
-    const uint4 a = kr[i], b = vr[i];                             // addresses (which spills)
-    *(uint4 *)(ktile + (lrow + i) * S::KS + lch * 8) =
-        make_uint4(a.x & mk, a.y & mk, a.z & mk, a.w & mk);
-    vw[i][0] = b.x & mk;
-    vw[i][1] = b.y & mk;
-    vw[i][2] = b.z & mk;
-    vw[i][3] = b.w & mk;
-  }
-  // V^T: dim d's four positions as one 8-byte store (halves picked by byte
-  // permutes), at the swizzled column of vt_col.
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-#pragma unroll
-    for (int odd = 0; odd < 2; ++odd) {
-      const uint32_t sel = odd ? 0x07060302u : 0x05040100u;
-      const uint32_t lo = __builtin_amdgcn_perm(vw[1][e], vw[0][e], sel);
-      const uint32_t hi = __builtin_amdgcn_perm(vw[3][e], vw[2][e], sel);
-      const int d = lch * 8 + 2 * e + odd;
-      *(uint2 *)(vtile + d * S::VS + vt_col<P>(d, lrow)) = make_uint2(lo, hi);
-    }
-  }
-  if constexpr (ROPE) {
-    __syncthreads();  // the tile row of `pos` holds the cache's old contents
-    if (owner && wave == hb % NW && lane < HD / 2) {
-      const int row = pos - t0;
-      ktile[row * S::KS + lane] = knew;
-      ktile[row * S::KS + lane + HD / 2] = knew2;
-      vtile[lane * S::VS + vt_col<P>(lane, row)] = vnew;
-      vtile[(lane + HD / 2) * S::VS + vt_col<P>(lane + HD / 2, row)] = vnew2;
-    }
-  }
-  __syncthreads();
+  for (int n = 0; n < ND; ++n) oc[n] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-  // ---- phase B: scores S[h][p] = q_h . k_p on MFMA (16x16x32 f16, f32
-  // accumulate): rows are the block's heads (up to 16; rows past hb carry
-  // whatever the LDS held and are never read back), columns 16 positions per
-  // tile, q as its f16 hi and lo parts so the products keep ~22 bits of q.
-  {
-    const int r16 = lane & 15, kq = (lane >> 4) * 8;
-    for (int nt = wave; nt < P / 16; nt += NW) {
-      f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int jt = 0; jt < NTL; ++jt) {
+    const int tt0 = t0 + jt * P;
+    if (tt0 >= tend) break;  // uniform
+    const int tt1 = min(tt0 + P, tend);
+    if (jt > 0) __syncthreads();  // every wave is done with the previous tile's LDS
+
+    // Tiles into LDS; rows past the cached positions are zero (their scores
+    // are masked, and a zero V row keeps 0 * v finite).
+    uint32_t vw[LD][4];
 #pragma unroll
-      for (int kk = 0; kk < HD; kk += 32) {
-        const h16x8 b = lds_h8(ktile + (nt * 16 + r16) * S::KS + kk + kq);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(qh + r16 * S::QS + kk + kq), b, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(ql + r16 * S::QS + kk + kq), b, c, 0, 0, 0);
+    for (int i = 0; i < LD; ++i) {
+      const uint32_t mk = tt0 + lrow + i < tt1 ? 0xFFFFFFFFu : 0u;  // a mask, not a select of
+      const uint4 a = kr[i], b = vr[i];                               // addresses (which spills)
+      *(uint4 *)(ktile + (lrow + i) * S::KS + lch * 8) =
+          make_uint4(a.x & mk, a.y & mk, a.z & mk, a.w & mk);
+      vw[i][0] = b.x & mk;
+      vw[i][1] = b.y & mk;
+      vw[i][2] = b.z & mk;
+      vw[i][3] = b.w & mk;
+    }
+    // V^T: dim d's four positions as one 8-byte store (halves picked by byte
+    // permutes), at the swizzled column of vt_col.
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int odd = 0; odd < 2; ++odd) {
+        const uint32_t sel = odd ? 0x07060302u : 0x05040100u;
+        const uint32_t lo = __builtin_amdgcn_perm(vw[1][e], vw[0][e], sel);
+        const uint32_t hi = __builtin_amdgcn_perm(vw[3][e], vw[2][e], sel);
+        const int d = lch * 8 + 2 * e + odd;
+        *(uint2 *)(vtile + d * S::VS + vt_col<P>(d, lrow)) = make_uint2(lo, hi);
       }
-      const int p = nt * 16 + r16;
-      const bool valid = t0 + p < t1;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[((lane >> 4) * 4 + i) * P + p] = valid ? c[i] : -INFINITY;
     }
-  }
-  __syncthreads();
-
-  // ---- phase C: softmax over the slice, a wave per head; the weights go to
-  // LDS as f16 hi and lo parts for the P.V MFMAs.
-  for (int hh = wave; hh < hb; hh += NW) {
-    constexpr int R = (P + 63) / 64;
-    float v[R];
-    float m = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int p = lane + 64 * r;
-      v[r] = p < P ? sc[hh * P + p] : -INFINITY;
-      m = fmaxf(m, v[r]);
-    }
-    m = wave_max(m);  // finite: every active slice holds a cached position
-    float l = 0.0f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int p = lane + 64 * r;
-      const float e = (v[r] == -INFINITY) ? 0.0f : __expf(v[r] - m);
-      const uint16_t eh = f2h(e);
-      if (p < P) {
-        ph[hh * S::PS + p] = eh;
-        pl[hh * S::PS + p] = f2h(e - h2f(eh));
+    // the next tile's loads go out now (the registers are consumed)
+    if (NTL > 1 && jt + 1 < NTL && tt0 + P < tend) load_tile(tt0 + P);
+    if constexpr (ROPE) {
+      const bool here = owner && pos >= tt0 && pos < tt1;  // uniform
+      if (here) {
+        __syncthreads();  // the tile row of `pos` holds the cache's old contents
+        if (wave == hb % NW && lane < HD / 2) {
+          const int row = pos - tt0;
+          ktile[row * S::KS + lane] = knew;
+          ktile[row * S::KS + lane + HD / 2] = knew2;
+          vtile[lane * S::VS + vt_col<P>(lane, row)] = vnew;
+          vtile[(lane + HD / 2) * S::VS + vt_col<P>(lane + HD / 2, row)] = vnew2;
+        }
       }
-      l += e;
     }
-    l = wave_sum(l);
-    if (lane == 0) {
-      ml[hh * 2] = m;
-      ml[hh * 2 + 1] = l;
+    __syncthreads();
+
+    // ---- phase B: scores S[h][p] = q_h . k_p on MFMA (16x16x32 f16, f32
+    // accumulate): rows are the block's heads (up to 16; rows past hb carry
+    // whatever the LDS held and are never read back), columns 16 positions per
+    // tile, q as its f16 hi and lo parts so the products keep ~22 bits of q.
+    {
+      const int r16 = lane & 15, kq = (lane >> 4) * 8;
+      for (int nt = wave; nt < P / 16; nt += NW) {
+        f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < HD; kk += 32) {
+          const h16x8 b = lds_h8(ktile + (nt * 16 + r16) * S::KS + kk + kq);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(qh + r16 * S::QS + kk + kq), b, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(ql + r16 * S::QS + kk + kq), b, c, 0, 0, 0);
+        }
+        const int p = nt * 16 + r16;
+        const bool valid = tt0 + p < tt1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[((lane >> 4) * 4 + i) * P + p] = valid ? c[i] : -INFINITY;
+      }
+    }
+    __syncthreads();
+
+    // ---- phase C: softmax over the tile, a wave per head, against the
+    // running maximum; the weights go to LDS as f16 hi and lo parts for the
+    // P.V MFMAs, and the running (m, l) and the accumulators' rescale to ml.
+    for (int hh = wave; hh < hb; hh += NW) {
+      constexpr int R = (P + 63) / 64;
+      float v[R];
+      float m = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int p = lane + 64 * r;
+        v[r] = p < P ? sc[hh * P + p] : -INFINITY;
+        m = fmaxf(m, v[r]);
+      }
+      m = wave_max(m);  // finite: every tile processed holds a cached position
+      const float m_old = ml[hh * 3];
+      const float mn = fmaxf(m_old, m);
+      const float corr = (m_old == -INFINITY) ? 0.0f : __expf(m_old - mn);
+      float l = 0.0f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int p = lane + 64 * r;
+        const float e = (v[r] == -INFINITY) ? 0.0f : __expf(v[r] - mn);
+        const uint16_t eh = f2h(e);
+        if (p < P) {
+          ph[hh * S::PS + p] = eh;
+          pl[hh * S::PS + p] = f2h(e - h2f(eh));
+        }
+        l += e;
+      }
+      l = wave_sum(l);
+      if (lane == 0) {
+        ml[hh * 3] = mn;
+        ml[hh * 3 + 1] = ml[hh * 3 + 1] * corr + l;
+        ml[hh * 3 + 2] = corr;
+      }
+    }
+    __syncthreads();
+
+    // ---- phase D: O[h][d] = corr_h O[h][d] + sum_p P[h][p] V[p][d] on MFMA
+    // (V^T rows are dims).
+    {
+      const int r16 = lane & 15, kq = (lane >> 4) * 8;
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        const int nd = wave + n * NW;
+        if (nd >= HD / 16) break;
+        const int d = nd * 16 + r16;
+        f32x4 c = oc[n];
+        if (NTL > 1) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int h = (lane >> 4) * 4 + i;
+            c[i] *= h < hb ? ml[h * 3 + 2] : 0.0f;
+          }
+        }
+#pragma unroll 4
+        for (int kk = 0; kk < P; kk += 32) {
+          const h16x8 b = lds_h8(vtile + d * S::VS + vt_col<P>(d, kk + kq));
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(ph + r16 * S::PS + kk + kq), b, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pl + r16 * S::PS + kk + kq), b, c, 0, 0, 0);
+        }
+        oc[n] = c;
+      }
     }
   }
-  __syncthreads();
 
-  // ---- phase D: O[h][d] = sum_p P[h][p] V[p][d] on MFMA (V^T rows are dims),
-  // then this slice's result straight from the accumulators.
+  // This slice's result straight from the accumulators.
   float *pacc = partials;
   float *pml = partials + (size_t)n_q * nsplit * HD;
   {
-    const int r16 = lane & 15, kq = (lane >> 4) * 8;
-    for (int nd = wave; nd < HD / 16; nd += NW) {
+    const int r16 = lane & 15;
+#pragma unroll
+    for (int n = 0; n < ND; ++n) {
+      const int nd = wave + n * NW;
+      if (nd >= HD / 16) break;
       const int d = nd * 16 + r16;
-      f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-      for (int kk = 0; kk < P; kk += 32) {
-        const h16x8 b = lds_h8(vtile + d * S::VS + vt_col<P>(d, kk + kq));
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(ph + r16 * S::PS + kk + kq), b, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pl + r16 * S::PS + kk + kq), b, c, 0, 0, 0);
-      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h = (lane >> 4) * 4 + i;
         if (h >= hb) continue;
         const size_t row = (size_t)(qh0 + h) * nsplit + split;
-        pacc[row * HD + d] = c[i];
+        pacc[row * HD + d] = oc[n][i];
         if (d == 0) {
-          pml[row * 2] = ml[h * 2];
-          pml[row * 2 + 1] = ml[h * 2 + 1];
+          pml[row * 2] = ml[h * 3];
+          pml[row * 2 + 1] = ml[h * 3 + 1];
         }
       }
     }
@@ -508,18 +593,18 @@ __global__ __launch_bounds__(32 * NL) void attn_merge_kernel(const float *__rest
   }
 }
 
-template <int HD, int P, bool ROPE>
+template <int HD, int P, bool ROPE, int NTL = 1>
 static void attn_go(const dim3 grid, const void *qkv, void *k_cache, void *v_cache,
                     void *partials, int n_q, int n_kv, const void *pos, int max_seq, float scale,
                     const RopeArgs &ra) {
   using S = AttnShape<HD, P>;
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute((const void *)attn_decode_kernel<HD, P, ROPE>,
+    (void)hipFuncSetAttribute((const void *)attn_decode_kernel<HD, P, ROPE, NTL>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS);
     attr_set = true;
   }
-  attn_decode_kernel<HD, P, ROPE><<<grid, S::T, S::LDS, WST_STREAM>>>(
+  attn_decode_kernel<HD, P, ROPE, NTL><<<grid, S::T, S::LDS, WST_STREAM>>>(
       (const float *)qkv, (uint16_t *)k_cache, (uint16_t *)v_cache, (float *)partials, n_q,
       n_kv, (const int32_t *)pos, max_seq, scale, ra);
 }
@@ -530,12 +615,21 @@ static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_ca
                         void *partials, void *out, int n_q, int n_kv, const void *pos,
                         int max_seq, float scale, const RopeArgs &ra, bool merge = true,
                         uint32_t *tw = nullptr) {
-  const int P = wst_attn_slice_len(head_dim, max_seq);
+  const int PT = attn_tile_len(head_dim), NTL = attn_tiles(head_dim, max_seq);
+  const int P = PT * NTL;  // positions per slice
   const int nsplit = (max_seq + P - 1) / P;
   const dim3 grid(n_kv, nsplit, attn_head_groups(n_q / n_kv, n_kv * nsplit));
 #define ATTN_GO(hd_, p_) attn_go<hd_, p_, ROPE>(grid, qkv, k_cache, v_cache, partials, n_q, \
                                                 n_kv, pos, max_seq, scale, ra)
-  switch (head_dim * 1000 + P) {
+#define ATTN_GO_T(hd_, p_, t_) attn_go<hd_, p_, ROPE, t_>(grid, qkv, k_cache, v_cache, partials, \
+                                                          n_q, n_kv, pos, max_seq, scale, ra)
+  switch (NTL > 1 ? -(head_dim * 10 + NTL) : head_dim * 1000 + PT) {
+    case -(64 * 10 + 2): ATTN_GO_T(64, 256, 2); break;
+    case -(64 * 10 + 3): ATTN_GO_T(64, 256, 3); break;
+    case -(64 * 10 + 4): ATTN_GO_T(64, 256, 4); break;
+    case -(128 * 10 + 2): ATTN_GO_T(128, 128, 2); break;
+    case -(128 * 10 + 3): ATTN_GO_T(128, 128, 3); break;
+    case -(128 * 10 + 4): ATTN_GO_T(128, 128, 4); break;
     case 64 * 1000 + 32: ATTN_GO(64, 32); break;
     case 64 * 1000 + 64: ATTN_GO(64, 64); break;
     case 64 * 1000 + 128: ATTN_GO(64, 128); break;
@@ -545,7 +639,7 @@ static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_ca
     case 128 * 1000 + 128: ATTN_GO(128, 128); break;
     default:
       if constexpr (!ROPE) {
-        if (P == 32) attn_go<256, 32, false>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv,
+        if (PT == 32) attn_go<256, 32, false>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv,
                                              pos, max_seq, scale, ra);
         else attn_go<256, 64, false>(grid, qkv, k_cache, v_cache, partials, n_q, n_kv, pos,
                                      max_seq, scale, ra);
@@ -553,6 +647,7 @@ static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_ca
       break;
   }
 #undef ATTN_GO
+#undef ATTN_GO_T
   if (merge) {
     const dim3 mg(n_q, head_dim / 32);
     const float *pa = (const float *)partials;
