@@ -11,25 +11,26 @@ told from a bug. No reference code is imported or run.
   05b   qwen05b_greedy.json: 0.5B shape, 16 prompt tokens, 64 greedy tokens.
   7b    qwen7b_ctx2048_greedy.json: the 7B shape of the headline benchmark,
         KV caches filled with the synthetic context (seed 2) for positions
-        0..2047, one seeded token at position 2048, 64 greedy tokens; plus a
+        0..2047, one seeded token at position 2048, 256 greedy tokens (the
+        configuration's 2048 -> 2304); plus a
         sample of the first step's logits (the top 64 and every 64th entry)
         and the oracle's two f32 summation orders (first-step logits and
-        their 64-token streams). About 4 minutes to pack on 8 threads, 4 s per
-        token.
+        their 256-token streams). About 4 minutes to pack on 8 threads, 4 s
+        per token and form.
   7bref adds to qwen7b_ctx2048_greedy.json the oracle's ORC_ACC_REF forward
         (the reference CUDA kernels' own arithmetic: f16 group sums in the
         GEMV, their reduction orders, attention split for a 30-SM device):
         its first-step logits at the same sample, its full-vector distance
-        from the f64-summing oracle, and its 64-token stream with margins;
-        the first step also at 132 SMs (another split count). About 15
-        minutes on 8 threads.
+        from the f64-summing oracle, and its 256-token stream with margins;
+        the first step also at 132 SMs (another split count). About an hour
+        on 8 threads.
   cfg2  qwen05b_ctx512_greedy.json: config 2's workload, the 0.5B shape with a
         seeded 512-token prompt and 256 greedy tokens (context 512 -> 768),
         plus the first generated step's logits under the oracle's two f32
         summation orders (the order-only drift at this depth).
   cfg4  qwen05b_qk_rescore_4096.json: the chunked-prefill configuration (0.5B
         shape, QK-norm, fp16 head rescore of the top 32), a seeded 4096-token
-        prompt, then 64 greedy tokens.
+        prompt, then 128 greedy tokens.
 """
 import json
 import sys
@@ -47,6 +48,8 @@ SEED = 0
 PROMPT_SEED = 1
 KV_SEED = 2
 N_NEW = 64
+N_NEW_7B = 256   # config 3: context 2048 -> 2304
+N_NEW_CFG4 = 128  # config 4: 128 decode steps after the prompt
 
 
 def _decode(st, nxt, lg, n):
@@ -91,7 +94,7 @@ def golden_7b():
     first = int(np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"]))
 
     def state():
-        st = O.State(m, ctx + N_NEW + 8, 0)
+        st = O.State(m, ctx + N_NEW_7B + 8, 0)
         st.fill_kv(KV_SEED, ctx)
         st.pos = ctx
         return st
@@ -102,12 +105,12 @@ def golden_7b():
             st = state()
             nxt_v, lg_v = st.step(first)
             drift[name] = lg_v.astype(np.float64)
-            variant_tokens[name] = _decode(st, nxt_v, lg_v, N_NEW)[0]
+            variant_tokens[name] = _decode(st, nxt_v, lg_v, N_NEW_7B)[0]
             st.close()
     st = state()
     nxt, lg = st.step(first)
     lg0 = lg.copy()
-    tokens, margins, top = _decode(st, nxt, lg, N_NEW)
+    tokens, margins, top = _decode(st, nxt, lg, N_NEW_7B)
     top64 = np.argsort(-lg0.astype(np.float64), kind="stable")[:64]
     every = np.arange(0, cfg["vocab"], 64)
     sample = np.unique(np.concatenate([top64, every]))
@@ -136,7 +139,7 @@ def golden_7b_ref():
     print(f"7b packed in {time.time() - t0:.0f}s", flush=True)
 
     def state():
-        st = O.State(m, ctx + N_NEW + 8, 0)
+        st = O.State(m, ctx + N_NEW_7B + 8, 0)
         st.fill_kv(g["kv_seed"], ctx)
         st.pos = ctx
         return st
@@ -160,7 +163,7 @@ def golden_7b_ref():
         ref = lg.astype(np.float64)
         print(f"7b ref first step {time.time() - t0:.0f}s: vs f64 {np.max(np.abs(ref - f64)):.4f}",
               flush=True)
-        tokens, margins, top = _decode(st, nxt, lg, N_NEW)
+        tokens, margins, top = _decode(st, nxt, lg, N_NEW_7B)
         st.close()
     g["ref"] = dict(
         sms=30,
@@ -210,12 +213,12 @@ def golden_cfg4():
     n_prompt = 4096
     m = O.Model(cfg, SEED)
     prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt)
-    st = O.State(m, n_prompt + N_NEW + 8, 0)
+    st = O.State(m, n_prompt + N_NEW_CFG4 + 8, 0)
     for i, t in enumerate(prompt):
         nxt, lg = st.step(int(t))
         if i % 512 == 511:
             print(f"cfg4 prompt {i + 1}/{n_prompt} ({time.time() - t0:.0f}s)", flush=True)
-    tokens, margins, top = _decode(st, nxt, lg, N_NEW)
+    tokens, margins, top = _decode(st, nxt, lg, N_NEW_CFG4)
     _write("qwen05b_qk_rescore_4096.json",
            dict(config="qwen2.5-0.5b-shape, qk_norm, rescore_k=32", seed=SEED,
                 prompt_seed=PROMPT_SEED, n_prompt=n_prompt, tokens=tokens, margins=margins,
