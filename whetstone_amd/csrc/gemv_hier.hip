@@ -632,6 +632,51 @@ __global__ __launch_bounds__(256) void gemv_hier_wide_kernel(
   }
 }
 
+// Measurement form (WST_GEMV_EXACT=1, plain GEMV only): the same row formula
+// with the activations as f16 values, not the 14-bit table: per group
+// Q = sum q_i x_i and S = sum x_i in f32 (each product exact), one wave per
+// row, lanes over groups l, l + 64, ..., then the wave sum. It exists to
+// measure what the table's rounding costs end to end; it is not fast.
+__global__ __launch_bounds__(256) void gemv_hier_exact_kernel(
+    const uint4 *__restrict__ qw, const uint8_t *__restrict__ si,
+    const uint32_t *__restrict__ sb, const uint16_t *__restrict__ x,
+    const uint16_t *__restrict__ bias, float *__restrict__ y, int in_f, int out_f, int accum) {
+  const int lane = threadIdx.x & 63, G = in_f / HGROUP;
+  for (int row = blockIdx.x * 4 + (threadIdx.x >> 6); row < out_f; row += gridDim.x * 4) {
+    float as = 0.0f, am = 0.0f;
+    for (int g = lane; g < G; g += 64) {
+      const size_t at = (size_t)row * G + g;
+      const uint4 p = qw[at];
+      const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+      float q = 0.0f, sx = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const float xv = h2f(x[(size_t)g * HGROUP + i]);
+        q = fmaf((float)((w[i / 8] >> (4 * (i % 8))) & 0xFu), xv, q);
+        sx += xv;
+      }
+      const uint32_t id = si[at];
+      as = fmaf((float)(id & 0xFu), q, as);
+      am = fmaf((float)(id >> 4), sx, am);
+    }
+    const uint32_t sv = sb[row];
+    float v = wave_sum(h2f((uint16_t)(sv & 0xFFFFu)) * as - h2f((uint16_t)(sv >> 16)) * am);
+    if (lane == 0) {
+      if (bias) v += h2f(bias[row]);
+      y[row] = accum ? y[row] + v : v;
+    }
+  }
+}
+
+static bool gemv_exact() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("WST_GEMV_EXACT");
+    v = e && e[0] == '1';
+  }
+  return v == 1;
+}
+
 // ---------------------------------------------------------------- dispatch
 
 // The (wide, huge, other) rule of the reference (gemv_hier.cu:253-272) picks
@@ -825,7 +870,12 @@ extern "C" wst_status_t wst_gemv_int4_hier_ex(const void *qw, const void *si, co
   const wst_status_t st = check_common(qw, si, sb, x, y, in_f, out_f, "wst_gemv_int4_hier");
   if (st != WST_OK) return st;
   const HierArgs a{qw, si, sb, x, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum, {}, {}};
-  if (!hier_dispatch<false, false>(a)) {
+  if (gemv_exact()) {
+    const int blocks = (out_f + 3) / 4, cap = wst_cu_count() * 8;
+    gemv_hier_exact_kernel<<<blocks < cap ? blocks : cap, 256, 0, WST_STREAM>>>(
+        (const uint4 *)qw, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
+        (const uint16_t *)bias, (float *)y, in_f, out_f, accum);
+  } else if (!hier_dispatch<false, false>(a)) {
     const int units = (out_f + 3) / 4;
     const int cap = wst_cu_count() * 16;
     gemv_hier_wide_kernel<4><<<units < cap ? units : cap, 256, 0, WST_STREAM>>>(
