@@ -86,6 +86,13 @@ def parse():
                    help="with --config 3: skip the configs 1, 2 and 4 measured after the "
                         "headline's timed region")
     p.add_argument("--stage-reps", type=int, default=20)
+    p.add_argument("--no-full-range", action="store_true",
+                   help="config 3: skip the timing of the whole 2048 -> 2304 range after the "
+                        "headline's steps")
+    p.add_argument("--no-graph", action="store_true",
+                   help="configs 2 and 3: launch each step's kernels eagerly instead of replaying "
+                        "the captured graph (the same kernels; for profiler runs, whose graph "
+                        "launch interception can crash)")
     p.add_argument("--max-seq", type=int, default=0,
                    help="KV-cache capacity for configs 2 and 3 (default: the context plus the "
                         "generated tokens plus 8); attention's grid covers the capacity")
@@ -735,8 +742,10 @@ def main():
         eng.prefill(prompt.astype(np.int32), chunked=True)
         workload = ("config 2: Qwen2.5-0.5B-shape int4 hier-g32 batch=1 greedy decode after a "
                     f"{ctx0}-token chunked prefill, context {ctx0} -> {ctx0 + a.steps}")
-    log(f"model ready ({t_gen:.2f}s), context {ctx0}; capturing the step graph")
-    eng.capture_graph()  # warm-up step + rewind inside
+    log(f"model ready ({t_gen:.2f}s), context {ctx0}; "
+        + ("eager steps" if a.no_graph else "capturing the step graph"))
+    if not a.no_graph:
+        eng.capture_graph()  # warm-up step + rewind inside
     log("graph captured; warm-up")
     tok0 = eng.token()
     for _ in range(a.warmup):
@@ -764,7 +773,7 @@ def main():
         bytes_steps.append(eng.step_bytes())
     bytes_tok = float(np.mean(bytes_steps))
     full = None
-    if a.config == 3 and a.steps != FULL_RANGE:
+    if a.config == 3 and a.steps != FULL_RANGE and not a.no_full_range:
         # the configuration's whole range, 2048 -> 2304, outside the timed region
         eng.set_pos(ctx0)
         eng.set_token(tok0)
@@ -814,7 +823,7 @@ def main():
                    "hbm_gbs": round(bytes_tok * tok_s / 1e9, 1),
                    "frac_of_hbm_peak": round(bytes_tok * tok_s / 1e9 / HBM_PEAK_GBS, 4),
                    "token_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bytes_tok, 1),
-                   "graph": True, "weights_generated_s": round(t_gen, 2)},
+                   "graph": not a.no_graph, "weights_generated_s": round(t_gen, 2)},
         "roofline": roofline,
         "kernels": kernels,
     }
