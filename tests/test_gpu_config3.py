@@ -117,19 +117,21 @@ def _first_divergence(a, b):
     return next((i for i, (x, y) in enumerate(zip(a, b)) if int(x) != int(y)), min(len(a), len(b)))
 
 
-def test_7b_greedy_stream_matches_golden_64_steps(model7b):
-    """The benchmark's own path: the captured step graph replayed per token.
+def test_7b_greedy_stream_matches_golden(model7b):
+    """The benchmark's own path: the captured step graph replayed per token,
+    over the configuration's range (the golden file's length: context 2048 ->
+    2304).
 
     Token identity is the bar, with the one exception the arithmetic forces:
     if two implementations' logits differ by at most delta everywhere, their
     argmaxes can differ only where the top-2 margin is at most 2 delta. At
     this depth the oracle with only its f32 summation order changed moves
     the logits by delta = 0.0146 (the golden file's first-step figure), so a
-    first divergence is accepted only at a step whose oracle top-2 margin is
-    below 2 delta. The golden file also holds the streams of the two f32
-    order variants; where those agree with each other for all 64 steps (they
-    do on these weights, both leaving the f64-summing mirrored stream at step
-    43), the GPU's stream must equal theirs token for token."""
+    first divergence is accepted only at a step whose top-2 margin (the
+    oracle's, or the compared stream's) is below 2 delta. Compared: the
+    f64-summing mirrored oracle's stream; the oracle's f32-summing forms'
+    streams (which leave the f64 stream at step 43 on these weights); and
+    the stream of the reference's own arithmetic (below)."""
     eng = _engine(model7b)
     eng.capture_graph()
     got = eng.generate(np.array([GOLDEN["first_token"]], np.int32), N_NEW, chunked=False)
@@ -146,13 +148,17 @@ def test_7b_greedy_stream_matches_golden_64_steps(model7b):
         assert margins[k] < 2 * delta, (
             f"diverged at step {k}: {got[k]} vs {want[k]}, oracle top-2 margin {margins[k]:.4g} "
             f">= 2 x order-only drift {delta:.4g}")
-    # Where the two f32-summing forms of the oracle agree with each other over
-    # all 64 steps, the GPU's stream is held to theirs, token for token.
-    seq, lane = (GOLDEN["order_variant_tokens"][k_] for k_ in ("f32_seq", "f32_lane"))
-    if list(seq) == list(lane):
-        kv = _first_divergence(got, seq)
-        print(f"7B greedy stream: {kv}/{N_NEW} tokens identical to the oracle's f32-summing forms")
-        assert kv == N_NEW, f"step {kv}: GPU {got[kv]} vs the oracle's f32 forms {seq[kv]}"
+    # The oracle's f32-summing forms: token identity up to a step where the
+    # form's own top-2 margin (its context equals the GPU's up to there) is
+    # below 2 delta.
+    for name in ("f32_seq", "f32_lane"):
+        toks = GOLDEN["order_variant_tokens"][name]
+        vm = GOLDEN.get("order_variant_margins", {}).get(name)
+        kv = _first_divergence(got, toks)
+        print(f"7B greedy stream: {kv}/{N_NEW} tokens identical to the oracle's {name} form")
+        if kv < N_NEW:
+            assert vm is not None and vm[kv] < 2 * delta, (
+                f"step {kv}: GPU {got[kv]} vs the oracle's {name} form {toks[kv]}")
     # Against the stream of the reference's own arithmetic (ORC_ACC_REF): its
     # logits are within d_ref of the f64 oracle's, the GPU's within d_gpu (the
     # first step's figures), so the two can pick different tokens only where
@@ -164,6 +170,6 @@ def test_7b_greedy_stream_matches_golden_64_steps(model7b):
           f"(which leaves the f64-summing oracle's at step "
           f"{_first_divergence(ref['tokens'], want)})")
     if kr < N_NEW:
-        assert ref["margins"][kr] < bound or margins[kr] < bound, (
-            f"diverged from the reference arithmetic at step {kr}: margins "
-            f"{ref['margins'][kr]:.4g} / {margins[kr]:.4g} >= {bound:.4g}")
+        assert ref["margins"][kr] < bound, (
+            f"diverged from the reference arithmetic at step {kr}: its top-2 margin "
+            f"{ref['margins'][kr]:.4g} >= {bound:.4g}")

@@ -2,7 +2,8 @@
 
 Qwen2.5-0.5B shape with QK-norm and the int4 head rescored from an fp16 copy
 (top 32); seeded weights packed on the device; a seeded 4096-token prompt
-prefilled in 256-token chunks (16 chunks), then 64 greedy tokens.
+prefilled in 256-token chunks (16 chunks), then the golden file's greedy
+tokens (128: the configuration's decode steps).
 
 The reference's contract for this path (crates/whetstone-core/src/engine.rs:
 195-199): chunked prefill gives bit-identical greedy output to sequential
