@@ -406,6 +406,25 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
   }
   __syncthreads();
 
+  // A lane's groups are the same for every unit, so with at most two groups
+  // per lane their table entries move to registers once, here, instead of
+  // being read from LDS for every unit (76 bytes per group and unit).
+  constexpr bool HOIST = NG <= 2;
+  uint4 hl[HOIST ? NG : 1][4];
+  int hc8[HOIST ? NG : 1];
+  float hS[HOIST ? NG : 1], hsc[HOIST ? NG : 1];
+  if constexpr (HOIST) {
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const uint32_t *e = xgt + (size_t)min(lr + j * LPR, G - 1) * XQ_WORDS;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hl[j][q] = *(const uint4 *)(e + 4 * q);
+      hc8[j] = (int)e[16];
+      hS[j] = __uint_as_float(e[17]);
+      hsc[j] = __uint_as_float(e[18]);
+    }
+  }
+
   // 5. rows. The trip count is the same for every wave of the block (the
   // WPR > 1 reduction synchronises the block).
   // Every block has at least one unit (the launch sizes the grid so), and a
@@ -432,11 +451,22 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     for (int j = 0; j < NG; ++j) {
       const int g = lr + j * LPR;
       if (g >= G) continue;
-      const uint32_t *e = xgt + (size_t)g * XQ_WORDS;
-      const uint4 l0 = *(const uint4 *)(e), l1 = *(const uint4 *)(e + 4);
-      const uint4 l2 = *(const uint4 *)(e + 8), l3 = *(const uint4 *)(e + 12);
-      const int c8 = (int)e[16];
-      const float S = __uint_as_float(e[17]), sc = __uint_as_float(e[18]);
+      uint4 l0, l1, l2, l3;
+      int c8;
+      float S, sc;
+      if constexpr (HOIST) {
+        l0 = hl[j][0]; l1 = hl[j][1]; l2 = hl[j][2]; l3 = hl[j][3];
+        c8 = hc8[j];
+        S = hS[j];
+        sc = hsc[j];
+      } else {
+        const uint32_t *e = xgt + (size_t)g * XQ_WORDS;
+        l0 = *(const uint4 *)(e); l1 = *(const uint4 *)(e + 4);
+        l2 = *(const uint4 *)(e + 8); l3 = *(const uint4 *)(e + 12);
+        c8 = (int)e[16];
+        S = __uint_as_float(e[17]);
+        sc = __uint_as_float(e[18]);
+      }
 #pragma unroll
       for (int k = 0; k < NR; ++k) {
         const uint4 p = B.wq[k][j];
