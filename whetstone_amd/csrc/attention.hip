@@ -485,10 +485,12 @@ __global__ __launch_bounds__(P_ * HD / 32) void attn_decode_kernel(
 // When the cache has at most 8 slices (SPREAD false), group 0 takes them all,
 // in slice order: the arithmetic of the merge inside the o GEMV (merge8 in
 // gemv_hier.hip), so both forms give the same bits.
-// A group's first ATTN_MERGE_BATCH slices are loaded together with the
-// position (slice indices clamped to the partials' extent), and slices past
-// the cached ones are replaced afterwards: up to 128 slices cost one memory
-// round trip per 16 NL slices.
+// A group's first B slices are loaded together with the position (slice
+// indices clamped to the partials' extent), and slices past the cached ones
+// are replaced afterwards: up to 128 slices cost one memory round trip per
+// B NL slices. With NL = 2, B is the smallest of 4, 8, 12, 16 that holds a
+// group's slices in one batch: fewer clamped loads, and the same bits as any
+// larger single batch (a dead slice adds exactly nothing).
 struct MergeState {
   float M, den, a;
 };
@@ -503,14 +505,13 @@ __device__ __forceinline__ void merge_combine(MergeState &x, const MergeState &y
   x.M = Mn;
 }
 
-template <int NL, bool SPREAD>
+template <int NL, bool SPREAD, int B = ATTN_MERGE_BATCH>
 __global__ __launch_bounds__(32 * NL) void attn_merge_kernel(const float *__restrict__ partials,
                                                          uint16_t *__restrict__ out, int n_q,
                                                          int hd, int nsplit,
                                                          const int32_t *__restrict__ pos_dev,
                                                          int max_seq, int P,
                                                          uint32_t *__restrict__ tw) {
-  constexpr int B = ATTN_MERGE_BATCH;
   __shared__ float hx[NL][32][3];
   __shared__ uint16_t mo[32];
   const int h = blockIdx.x, d0 = blockIdx.y * 32, tid = threadIdx.x;
@@ -653,12 +654,15 @@ static void attn_launch(int head_dim, const void *qkv, void *k_cache, void *v_ca
     const float *pa = (const float *)partials;
     const int32_t *pp = (const int32_t *)pos;
     uint16_t *o = (uint16_t *)out;
-    if (nsplit <= 8)
-      attn_merge_kernel<2, false><<<mg, 64, 0, WST_STREAM>>>(pa, o, n_q, head_dim, nsplit, pp,
-                                                               max_seq, P, tw);
-    else if (nsplit <= 2 * ATTN_MERGE_BATCH)
-      attn_merge_kernel<2, true><<<mg, 64, 0, WST_STREAM>>>(pa, o, n_q, head_dim, nsplit, pp,
-                                                              max_seq, P, tw);
+#define ATTN_MERGE(sp_, b_)                                                              \
+  attn_merge_kernel<2, sp_, b_><<<mg, 64, 0, WST_STREAM>>>(pa, o, n_q, head_dim, nsplit, pp, \
+                                                          max_seq, P, tw)
+    if (nsplit <= 4) ATTN_MERGE(false, 4);
+    else if (nsplit <= 8) ATTN_MERGE(false, 8);
+    else if (nsplit <= 16) ATTN_MERGE(true, 8);
+    else if (nsplit <= 24) ATTN_MERGE(true, 12);
+    else if (nsplit <= 2 * ATTN_MERGE_BATCH) ATTN_MERGE(true, 16);
+#undef ATTN_MERGE
     else
       attn_merge_kernel<ATTN_MERGE_LANES, true><<<mg, 32 * ATTN_MERGE_LANES, 0, WST_STREAM>>>(
           pa, o, n_q, head_dim, nsplit, pp, max_seq, P, tw);

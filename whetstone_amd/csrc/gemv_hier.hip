@@ -139,15 +139,18 @@ struct AttnIn {
 // batch: every live slice in slice order, after the batch's maximum). Every
 // load is issued unconditionally (slice indices clamped), then dead slices
 // are replaced by select.
+// MS: the slices read (4 or AM_MAX_SLICES); slices past nsplit are clamped
+// and replaced, so a cache of at most 4 slices gives the same bits either way.
+template <int MS>
 __device__ __forceinline__ uint4 merge8(const AttnIn &am, const float *partials, int b) {
   const int c0 = 8 * b, h = c0 / am.hd, d0 = c0 % am.hd;
   const float *pacc = partials;
   const float *pml = partials + (size_t)am.n_q * am.nsplit * am.hd;
   const size_t row0 = (size_t)h * am.nsplit;
   const int pos = *am.pos;
-  float ms[AM_MAX_SLICES], ls[AM_MAX_SLICES], vs[AM_MAX_SLICES][8];
+  float ms[MS], ls[MS], vs[MS][8];
 #pragma unroll
-  for (int sl = 0; sl < AM_MAX_SLICES; ++sl) {
+  for (int sl = 0; sl < MS; ++sl) {
     const size_t r = row0 + min(sl, am.nsplit - 1);
     const float2 mlv = *(const float2 *)(pml + r * 2);
     ms[sl] = mlv.x;
@@ -161,7 +164,7 @@ __device__ __forceinline__ uint4 merge8(const AttnIn &am, const float *partials,
   const int nactive = (seq + am.P - 1) / am.P;
   float M = -INFINITY;
 #pragma unroll
-  for (int sl = 0; sl < AM_MAX_SLICES; ++sl) {
+  for (int sl = 0; sl < MS; ++sl) {
     const bool live = sl < nactive;
     ms[sl] = live ? ms[sl] : -INFINITY;
     ls[sl] = live ? ls[sl] : 0.0f;
@@ -169,10 +172,10 @@ __device__ __forceinline__ uint4 merge8(const AttnIn &am, const float *partials,
     for (int e = 0; e < 8; ++e) vs[sl][e] = live ? vs[sl][e] : 0.0f;
     M = fmaxf(M, ms[sl]);
   }
-  float f[AM_MAX_SLICES];  // one exp per slice, shared by the eight columns
+  float f[MS];  // one exp per slice, shared by the eight columns
   float den = 0.0f;         // the merge kernel's a *= 0, den *= 0 from -inf
 #pragma unroll
-  for (int sl = 0; sl < AM_MAX_SLICES; ++sl) {
+  for (int sl = 0; sl < MS; ++sl) {
     f[sl] = (ms[sl] == -INFINITY) ? 0.0f : __expf(ms[sl] - M);
     den = fmaf(ls[sl], f[sl], den);
   }
@@ -181,7 +184,7 @@ __device__ __forceinline__ uint4 merge8(const AttnIn &am, const float *partials,
   for (int e = 0; e < 8; ++e) {
     float a = 0.0f;
 #pragma unroll
-    for (int sl = 0; sl < AM_MAX_SLICES; ++sl) a = fmaf(vs[sl][e], f[sl], a);
+    for (int sl = 0; sl < MS; ++sl) a = fmaf(vs[sl][e], f[sl], a);
     o[e] = f2h(a / den);
   }
   return make_uint4(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16),
@@ -247,7 +250,7 @@ __device__ __forceinline__ float slot_sum(float v) {
 // wave, so a wave streams RPW rows at once.
 // AX: the argmax epilogue above (plain rows only).
 template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW = 1,
-          bool AM = false, bool AX = false, bool XT = false, bool TW = false>
+          int AM = 0, bool AX = false, bool XT = false, bool TW = false>
 __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     const uint4 *qw, const uint8_t *si,
     const uint32_t *__restrict__ sb, const void *xin,
@@ -307,7 +310,7 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       xf[i][4] = c.x; xf[i][5] = c.y; xf[i][6] = c.z; xf[i][7] = c.w;
       nwv[i] = *(const uint4 *)(norm_w + (size_t)bc * 8);
     } else if constexpr (AM) {
-      xh[i] = merge8(am, (const float *)xin, min(b, NB8 - 1));
+      xh[i] = merge8<AM>(am, (const float *)xin, min(b, NB8 - 1));
     } else {
       xh[i] = *(const uint4 *)((const uint16_t *)xin + (size_t)min(b, NB8 - 1) * 8);
     }
@@ -778,7 +781,7 @@ static int gemv_pd_override() {
   return v;
 }
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW, bool AM,
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW, int AM,
           bool AX, bool XT, bool TW>
 static void launch_pd(const HierArgs &a) {
   auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW, AM, AX, XT, TW>;
@@ -811,7 +814,7 @@ static void launch_pd(const HierArgs &a) {
       a.in_f, a.nunits, a.accum, a.am, a.ax, a.tw);
 }
 
-template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1, bool AM = false,
+template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1, int AM = 0,
           bool AX = false, bool XT = false, bool TW = false>
 static void launch_q(const HierArgs &a) {
   if constexpr (TW) {  // the table epilogue runs with one unit in flight
@@ -840,7 +843,7 @@ static int gemv_rpw_override() {
 // long rows use 1024 so a CU builds its table once.
 #define GEMV_MAX_G 1280  // groups per row handled by the table kernel
 
-template <bool NORM, bool SWIGLU, bool AM = false, bool AX = false, bool XT = false,
+template <bool NORM, bool SWIGLU, int AM = 0, bool AX = false, bool XT = false,
           bool TW = false>
 static bool hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
@@ -983,7 +986,7 @@ extern "C" wst_status_t wst_gemv_hier_xq(const void *qw, const void *si, const v
   const wst_status_t st = check_common(qw, si, sb, table, y, in_f, out_f, "wst_gemv_hier_xq");
   if (st != WST_OK) return st;
   const HierArgs a{qw, si, sb, table, nullptr, 0.0f, nullptr, bias, y, in_f, out_f, accum, {}, {}};
-  if (!hier_dispatch<false, false, false, false, true>(a)) {
+  if (!hier_dispatch<false, false, 0, false, true>(a)) {
     snprintf(wst_err_buf, sizeof(wst_err_buf), "wst_gemv_hier_xq: in_features above 40960");
     return WST_ERR_SHAPE;
   }
@@ -1009,8 +1012,8 @@ extern "C" wst_status_t wst_gemv_hier_swiglu_xq(const void *qw, const void *si, 
   WST_REQUIRE(!((uintptr_t)norm_w & 15u), "wst_gemv_hier_swiglu_xq: norm weight must be 16-byte aligned");
   HierArgs a{qw, si, sb, x, norm_w, eps, nullptr, nullptr, out, in_f, inter, 0, {}, {}};
   a.tw = (uint32_t *)table;
-  if (norm_w) hier_dispatch<true, true, false, false, false, true>(a);
-  else hier_dispatch<false, true, false, false, false, true>(a);
+  if (norm_w) hier_dispatch<true, true, 0, false, false, true>(a);
+  else hier_dispatch<false, true, 0, false, false, true>(a);
   WST_TRY_KERNEL("wst_gemv_hier_swiglu_xq");
   return WST_OK;
 }
@@ -1035,7 +1038,9 @@ extern "C" wst_status_t wst_gemv_hier_attn(const void *qw, const void *si, const
   WST_REQUIRE(nsplit <= AM_MAX_SLICES, "wst_gemv_hier_attn: more than 8 attention slices");
   HierArgs a{qw, si, sb, partials, nullptr, 0.0f, nullptr, nullptr, y, in_f, out_f, accum,
              {(const int32_t *)pos, nsplit, head_dim, n_q, max_seq, P}, {}};
-  if (!hier_dispatch<false, false, true>(a)) {
+  const bool ok = nsplit <= 4 ? hier_dispatch<false, false, 4>(a)
+                              : hier_dispatch<false, false, AM_MAX_SLICES>(a);
+  if (!ok) {
     snprintf(wst_err_buf, sizeof(wst_err_buf), "wst_gemv_hier_attn: in_features above 40960");
     return WST_ERR_SHAPE;
   }
@@ -1063,7 +1068,7 @@ extern "C" wst_status_t wst_gemv_hier_rmsnorm_argmax(const void *qw, const void 
   if (!sc) return WST_ERR_OOM;
   const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, nullptr, y, in_f, out_f, 0, {},
                    {(int32_t *)out_idx, (int32_t *)pos, max_seq, sc}};
-  hier_dispatch<true, false, false, true>(a);
+  hier_dispatch<true, false, 0, true>(a);
   WST_TRY_KERNEL("wst_gemv_hier_rmsnorm_argmax");
   return WST_OK;
 }
