@@ -83,13 +83,13 @@ wst_status_t wst_attn_decode_fused(void *qkv, void *k_cache, void *v_cache,
 
 /* wst_gemv_hier_rmsnorm(W, x, norm_w, eps, h_out, bias NULL, y, accum 0)
  * followed by wst_argmax_advance(y, out_idx, out_f, pos, max_seq), in one
- * launch: the GEMV's blocks keep the argmax key of the rows they write and
- * the last block to finish combines them (pos NULL: no advance). The step's
- * head when nothing (rescore) runs between the logits and the argmax.
- * Its group maxima and arrival counters live in one library scratch slot per
- * device, shared by every stream: calls on one GPU must not overlap (issue
- * them on one stream, or order them), or a call can miss its final combine
- * and leave out_idx unwritten. */
+ * call: the GEMV's blocks store the argmax key of the rows they write, and a
+ * one-block kernel after it takes their maximum, writes out_idx and advances
+ * pos (pos NULL: no advance). The step's head when nothing (rescore) runs
+ * between the logits and the argmax. The per-block keys live in one library
+ * scratch slot per device, shared by every stream: calls on one GPU must not
+ * overlap (issue them on one stream, or order them), or one call can read
+ * another's keys. */
 wst_status_t wst_gemv_hier_rmsnorm_argmax(const void *qw, const void *si, const void *sb,
                                           const void *x, const void *norm_w, float eps,
                                           void *h_out, void *y, int32_t in_f, int32_t out_f,

@@ -191,24 +191,18 @@ __device__ __forceinline__ uint4 merge8(const AttnIn &am, const float *partials,
                     o[4] | ((uint32_t)o[5] << 16), o[6] | ((uint32_t)o[7] << 16));
 }
 
-// The argmax epilogue (AX forms). Every block folds the argmax keys of the
-// rows it wrote into one of AX_GROUPS group maxima (block % AX_GROUPS) with a
-// relaxed agent-scope atomic max, then counts itself in the group; the last
-// block of a group folds the group maximum into the total and counts the
-// group; the last group's block writes the token, advances the position and
-// leaves every maximum and counter at zero for the next launch. Each atomic
-// waits for the previous one's result (the count's increment depends on it),
-// so a maximum is in place before the count that announces it; no cache
-// write-back or invalidate is needed, since only atomics touch these words.
-#define AX_GROUPS 8
-struct AxScratch {
-  unsigned long long gmax[AX_GROUPS], total;
-  unsigned int gcount[AX_GROUPS], count;
-};
+// The argmax epilogue (AX forms). Every block stores the largest argmax key
+// of the rows it wrote (the order-preserving key of sample.cu:28-37) to its
+// own slot of `keys`, a plain store; a one-block kernel launched after the
+// GEMV takes the maximum of the slots, writes the token and advances the
+// position. (An earlier form folded the keys with chains of agent-scope
+// atomics into group maxima, the last block finishing: about 6 us on the 0.5B
+// head, against about 2 us for the second launch.)
+#define AX_MAX_BLOCKS 8192
 struct ArgmaxOut {
   int32_t *out, *pos;
   int max_seq;
-  AxScratch *sc;
+  unsigned long long *keys;  // [gridDim.x]
 };
 
 // Sum over a row's lanes when a row spans LPR <= 64 lanes of one wave (every
@@ -566,36 +560,31 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       unsigned long long b = wbest[0];
 #pragma unroll
       for (int w = 1; w < NW; ++w) b = wbest[w] > b ? wbest[w] : b;
-      const int g = blockIdx.x % AX_GROUPS;
-      const int ng = (int)gridDim.x < AX_GROUPS ? (int)gridDim.x : AX_GROUPS;
-      const unsigned int members = (gridDim.x - g + AX_GROUPS - 1) / AX_GROUPS;
-      const unsigned long long m0 =
-          __hip_atomic_fetch_max(&ax.sc->gmax[g], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // (m0 == ~0ull never happens: no key has every bit set) -- the branch
-      // makes the count wait for the maximum's completion
-      const unsigned int inc = m0 == ~0ull ? 2u : 1u;
-      const unsigned int c =
-          __hip_atomic_fetch_add(&ax.sc->gcount[g], inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (c + 1 == members) {
-        const unsigned long long gm =
-            __hip_atomic_exchange(&ax.sc->gmax[g], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&ax.sc->gcount[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long t0 =
-            __hip_atomic_fetch_max(&ax.sc->total, gm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned int inc2 = t0 == ~0ull ? 2u : 1u;
-        const unsigned int c2 =
-            __hip_atomic_fetch_add(&ax.sc->count, inc2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((int)c2 + 1 == ng) {
-          const unsigned long long tot =
-              __hip_atomic_exchange(&ax.sc->total, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(&ax.sc->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          *ax.out = (int32_t)(~(uint32_t)(tot & 0xFFFFFFFFull));
-          if (ax.pos) {
-            const int p = *ax.pos + 1;
-            *ax.pos = p < ax.max_seq ? p : ax.max_seq;
-          }
-        }
-      }
+      ax.keys[blockIdx.x] = b;
+    }
+  }
+}
+
+// The argmax over the head blocks' keys (one block of 1024 threads), then
+// the token and the position advance.
+__global__ __launch_bounds__(1024) void argmax_keys_kernel(
+    const unsigned long long *__restrict__ keys, int n, int32_t *__restrict__ out,
+    int32_t *__restrict__ pos, int max_seq) {
+  __shared__ unsigned long long wbest[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  unsigned long long b = 0ull;
+  for (int i = tid; i < n; i += 1024) b = keys[i] > b ? keys[i] : b;
+  b = wave_max_u64(b);
+  if (lane == 0) wbest[wave] = b;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long m = wbest[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) m = wbest[w] > m ? wbest[w] : m;
+    *out = (int32_t)(~(uint32_t)(m & 0xFFFFFFFFull));
+    if (pos) {
+      const int p = *pos + 1;
+      *pos = p < max_seq ? p : max_seq;
     }
   }
 }
@@ -783,7 +772,7 @@ static int gemv_pd_override() {
 
 template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int PD, int RPW, int AM,
           bool AX, bool XT, bool TW>
-static void launch_pd(const HierArgs &a) {
+static int launch_pd(const HierArgs &a) {
   auto kern = gemv_hier_kernel<NG, WPR, XB, NT, NORM, SWIGLU, PD, RPW, AM, AX, XT, TW>;
   size_t lds = (size_t)(a.in_f / HGROUP) * XQ_WORDS * 4;
   if (XT && lds < (size_t)XT_CHUNKS(XB) * NT * 16) lds = (size_t)XT_CHUNKS(XB) * NT * 16;
@@ -808,28 +797,31 @@ static void launch_pd(const HierArgs &a) {
     const int full = wst_cu_count() * q_res, need = (a.nunits + PER - 1) / PER;
     grid = full < need ? full : need;
   }
+  // AX: one key slot per block (the grid is persistent: fewer blocks cover
+  // every unit)
+  if (AX && grid > AX_MAX_BLOCKS) grid = AX_MAX_BLOCKS;
   kern<<<grid, NT, lds, WST_STREAM>>>(
       (const uint4 *)a.qw, (const uint8_t *)a.si, (const uint32_t *)a.sb, a.x,
       (const uint16_t *)a.norm_w, a.eps, (uint16_t *)a.h_out, (const uint16_t *)a.bias, a.y,
       a.in_f, a.nunits, a.accum, a.am, a.ax, a.tw);
+  return grid;
 }
 
 template <int NG, int WPR, int XB, int NT, bool NORM, bool SWIGLU, int RPW = 1, int AM = 0,
           bool AX = false, bool XT = false, bool TW = false>
-static void launch_q(const HierArgs &a) {
+static int launch_q(const HierArgs &a) {
   if constexpr (TW) {  // the table epilogue runs with one unit in flight
-    launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX, XT, TW>(a);
-    return;
+    return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX, XT, TW>(a);
   } else {
     int pd = gemv_pd_override();
     if (pd < 1 || pd > 4) {
       const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR * RPW);
       pd = a.nunits >= 8 * slots ? 2 : 1;
     }
-    if (pd == 1) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX, XT, TW>(a);
-    else if (pd == 3) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM, AX, XT, TW>(a);
-    else if (pd == 4) launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW, AM, AX, XT, TW>(a);
-    else launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW, AM, AX, XT, TW>(a);
+    if (pd == 1) return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX, XT, TW>(a);
+    if (pd == 3) return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM, AX, XT, TW>(a);
+    if (pd == 4) return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 4, RPW, AM, AX, XT, TW>(a);
+    return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 2, RPW, AM, AX, XT, TW>(a);
   }
 }
 
@@ -845,7 +837,8 @@ static int gemv_rpw_override() {
 
 template <bool NORM, bool SWIGLU, int AM = 0, bool AX = false, bool XT = false,
           bool TW = false>
-static bool hier_dispatch(const HierArgs &a) {
+// Returns the grid launched, 0 when in_f is outside the table kernel.
+static int hier_dispatch(const HierArgs &a) {
   const int G = a.in_f / HGROUP;
   // Rows of at most 32 groups (in_f <= 1024, e.g. the 0.5B hidden 896) share a
   // wave: with one row per wave, 28 groups left 36 of 64 lanes idle and a
@@ -856,23 +849,22 @@ static bool hier_dispatch(const HierArgs &a) {
   // tok/s), so four is the default for every shape (a row's bits must not
   // depend on the output count). WST_GEMV_RPW=1|2|8 selects the others.
   const int rpw = gemv_rpw_override();
-  if (G <= 16 && rpw != 1) launch_q<1, 1, 1, 512, NORM, SWIGLU, 4, AM, AX, XT, TW>(a);
-  else if (G <= 32 && rpw == 2) launch_q<1, 1, 1, 512, NORM, SWIGLU, 2, AM, AX, XT, TW>(a);
-  else if (G <= 32 && rpw == 8) launch_q<4, 1, 1, 512, NORM, SWIGLU, 8, AM, AX, XT, TW>(a);
-  else if (G <= 32 && rpw != 1) launch_q<2, 1, 1, 512, NORM, SWIGLU, 4, AM, AX, XT, TW>(a);
-  else if (G <= 64) launch_q<1, 1, 1, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
-  else if (G <= 128) launch_q<2, 1, 1, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
-  else if (G <= 192) launch_q<3, 1, 2, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
-  else if (G <= 256) launch_q<4, 1, 2, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+  if (G <= 16 && rpw != 1) return launch_q<1, 1, 1, 512, NORM, SWIGLU, 4, AM, AX, XT, TW>(a);
+  else if (G <= 32 && rpw == 2) return launch_q<1, 1, 1, 512, NORM, SWIGLU, 2, AM, AX, XT, TW>(a);
+  else if (G <= 32 && rpw == 8) return launch_q<4, 1, 1, 512, NORM, SWIGLU, 8, AM, AX, XT, TW>(a);
+  else if (G <= 32 && rpw != 1) return launch_q<2, 1, 1, 512, NORM, SWIGLU, 4, AM, AX, XT, TW>(a);
+  else if (G <= 64) return launch_q<1, 1, 1, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+  else if (G <= 128) return launch_q<2, 1, 1, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+  else if (G <= 192) return launch_q<3, 1, 2, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+  else if (G <= 256) return launch_q<4, 1, 2, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
   else if constexpr (NORM) {
-    if (G <= 512) launch_q<4, 2, 4, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
-    else return false;
+    if (G <= 512) return launch_q<4, 2, 4, 512, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+    else return 0;
   } else {
-    if (G <= 640) launch_q<5, 2, 3, 1024, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
-    else if (G <= GEMV_MAX_G) launch_q<5, 4, 5, 1024, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
-    else return false;
+    if (G <= 640) return launch_q<5, 2, 3, 1024, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+    else if (G <= GEMV_MAX_G) return launch_q<5, 4, 5, 1024, NORM, SWIGLU, 1, AM, AX, XT, TW>(a);
+    else return 0;
   }
-  return true;
 }
 
 static wst_status_t check_common(const void *qw, const void *si, const void *sb, const void *x,
@@ -1064,11 +1056,16 @@ extern "C" wst_status_t wst_gemv_hier_rmsnorm_argmax(const void *qw, const void 
   WST_REQUIRE(in_f / HGROUP <= 512, "wst_gemv_hier_rmsnorm_argmax: in_features above 16384");
   WST_REQUIRE(!(((uintptr_t)norm_w | (uintptr_t)h_out) & 15u),
               "wst_gemv_hier_rmsnorm_argmax: norm weight and h must be 16-byte aligned");
-  AxScratch *sc = (AxScratch *)wst_static_scratch(WST_SCRATCH_HEADMAX, sizeof(AxScratch));
-  if (!sc) return WST_ERR_OOM;
+  unsigned long long *keys = (unsigned long long *)wst_static_scratch(
+      WST_SCRATCH_HEADMAX, AX_MAX_BLOCKS * sizeof(unsigned long long));
+  if (!keys) return WST_ERR_OOM;
   const HierArgs a{qw, si, sb, x, norm_w, eps, h_out, nullptr, y, in_f, out_f, 0, {},
-                   {(int32_t *)out_idx, (int32_t *)pos, max_seq, sc}};
-  hier_dispatch<true, false, 0, true>(a);
+                   {(int32_t *)out_idx, (int32_t *)pos, max_seq, keys}};
+  const int nblocks = hier_dispatch<true, false, 0, true>(a);
+  WST_REQUIRE(nblocks > 0 && nblocks <= AX_MAX_BLOCKS,
+              "wst_gemv_hier_rmsnorm_argmax: grid outside the key slots");
+  argmax_keys_kernel<<<1, 1024, 0, WST_STREAM>>>(keys, nblocks, (int32_t *)out_idx,
+                                                 (int32_t *)pos, max_seq);
   WST_TRY_KERNEL("wst_gemv_hier_rmsnorm_argmax");
   return WST_OK;
 }
