@@ -452,8 +452,8 @@ def secondary_configs(E, wk) -> dict:
 def floors_bench(E, wk, config: int, reps: int) -> None:
     """The floor of the decode step's launch structure: a captured graph with
     one launch per kernel of the fused step (per layer: norm+qkv, attention
-    slices, slice merge, o, norm+gate|up+SwiGLU, down; then the head with its
-    argmax, and the embedding row), each launch replaced by the library's
+    slices, slice merge, o, norm+gate|up+SwiGLU, down; then the head, the
+    argmax over its blocks' keys, and the embedding row), each launch replaced by the library's
     plain streaming read (wst_stream_read) of that kernel's algorithmic bytes
     from its own buffer (so the weights stream cold, as in the step); and a
     graph of the same number of minimal launches (16 bytes each), which is
@@ -479,7 +479,8 @@ def floors_bench(E, wk, config: int, reps: int) -> None:
         stage_bytes["o"] += stage_bytes.pop("merge") - nq * hd * 2
     head_bytes = V * row(H) + H * 8 + V * 4
     per_layer = [(k, -(-b // 256) * 256) for k, b in stage_bytes.items()]
-    total = sum(b for _, b in per_layer) * L + head_bytes + H * 4
+    keys_bytes = 4096  # the argmax finish: one 8-byte key per head block
+    total = sum(b for _, b in per_layer) * L + head_bytes + keys_bytes + H * 4
     buf = wk.DeviceBuffer(total + 4096, np.uint8)
     ffi.call("wst_memset", buf.ptr, 1, total + 4096)
     sink = wk.DeviceBuffer(4, np.float32)
@@ -492,6 +493,8 @@ def floors_bench(E, wk, config: int, reps: int) -> None:
             off += b
     launches.append((off, -(-head_bytes // 256) * 256))
     off += launches[-1][1]
+    launches.append((off, keys_bytes))  # the argmax over the head blocks' keys
+    off += keys_bytes
     launches.append((off, H * 4))  # the next step's embedding row
     wk.synchronize()
 
@@ -524,7 +527,7 @@ def floors_bench(E, wk, config: int, reps: int) -> None:
         "value": round(1.0 / t_stream, 1), "unit": "tok/s", "n_gpus": 1,
         "higher_is_better": True, "data": "synthetic (streaming reads of each kernel's bytes)",
         "config": {"workload": f"config {config}: {n} dependent launches per token "
-                               f"({L} layers x {len(per_layer)} + head + embedding), context "
+                               f"({L} layers x {len(per_layer)} + head + argmax + embedding), context "
                                f"{ctx}, as one captured graph",
                    "bytes_per_token": total,
                    "stream_graph_us_per_token": round(t_stream * 1e6, 1),
