@@ -16,8 +16,6 @@ guard the emulation itself: numpy's f16 rounding against the definition on
 every f16 midpoint, and a planted case where one rounding (fma) and two
 (multiply, then add) give different f16 results.
 """
-import ctypes as C
-
 import numpy as np
 import pytest
 
@@ -318,3 +316,28 @@ def test_ref_forward_close_to_f64():
             st.close()
     d = np.max(np.abs(lgs[O.ACC_F64] - lgs[O.ACC_REF]))
     assert 0 < d < 2e-2
+
+
+def test_ref_gemv_overflowing_group_sum_matches_emulation():
+    """x large enough that an f16 group partial overflows to inf: the oracle
+    leaves its integer fast path for the f16 one, and still follows the
+    kernel (inf enters the row sum; the other rows are unaffected)."""
+    in_f, out_f = 64, 4
+    rng = np.random.default_rng(11)
+    w = rng.standard_normal((out_f, in_f)).astype(np.float32) * 0.02
+    p, _ = O.quantize(w, in_f, out_f)
+    x = (rng.standard_normal(in_f) * 0.5).astype(np.float16)
+    x[3] = np.float16(60000.0)
+    x[35] = np.float16(-60000.0)
+    with O.variant(O.ACC_REF):
+        got = O.gemv(p, x.view(np.uint16))
+    qw = p.qw.reshape(out_f, in_f // 8)
+    si = p.si.reshape(out_f, in_f // 32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        for r in range(out_f):
+            want = np.float32(emulate_gemv_row(qw[r], si[r], int(p.sb[r]), x))
+            if np.isnan(want):
+                assert np.isnan(got[r]), (r, got[r])
+            else:
+                assert got[r].view(np.uint32) == want.view(np.uint32), (r, got[r], want)
+    assert not np.all(np.isfinite(got))  # the overflow is exercised
