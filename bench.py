@@ -96,6 +96,8 @@ def parse():
     p.add_argument("--max-seq", type=int, default=0,
                    help="KV-cache capacity for configs 2 and 3 (default: the context plus the "
                         "generated tokens plus 8); attention's grid covers the capacity")
+    p.add_argument("--batched-only", action="store_true",
+                   help="with --config 4: time only the batched prefill (for profiler runs)")
     p.add_argument("--gemm-7b", action="store_true",
                    help="with --config 4: also time the chunk GEMMs at the 7B shapes")
     p.add_argument("--floors", action="store_true",
@@ -319,7 +321,7 @@ def chunk_gemm_times(wk, shapes, n: int = 256, reps: int = 50) -> dict:
 
 
 def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False, gemms: bool = True,
-                  emit: bool = True) -> dict:
+                  emit: bool = True, batched_only: bool = False) -> dict:
     """Config 4: chunked prefill of 4096 tokens (256 per chunk), then n_new
     graph decode steps (none, and no graph capture, for n_new = 0)."""
     cfg = dict(E.QWEN05B, qk_norm=1, rescore_k=32)
@@ -327,14 +329,28 @@ def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False, gemms: bool = True,
     g = E.Model(cfg, seed=WEIGHT_SEED)
     eng = E.Engine(g, n_prompt + n_new + 8)
     ids = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt).astype(np.int32)
-    eng.prefill(ids[:chunk], chunked=True)  # warm-up (kernels, scratch), then rewind
-    eng.set_pos(0)
-    wk.synchronize()
-    log(f"prefill {n_prompt} tokens in {chunk}-token chunks")
-    t0 = time.perf_counter()
-    eng.prefill(ids, chunked=True)
-    wk.synchronize()
-    dt_p = time.perf_counter() - t0
+    def timed_prefill(batch: bool) -> float:
+        # The full chunks share each layer's launches unless batch is off
+        # (WSE_CHUNK_BATCH=0: one launch per chunk and op); the bits are the
+        # same either way. A warm-up prefill first (kernels, buffers, split
+        # scratch), then rewind.
+        os.environ["WSE_CHUNK_BATCH"] = "1" if batch else "0"
+        try:
+            eng.set_pos(0)
+            eng.prefill(ids, chunked=True)
+            eng.set_pos(0)
+            wk.synchronize()
+            t0 = time.perf_counter()
+            eng.prefill(ids, chunked=True)
+            wk.synchronize()
+            return time.perf_counter() - t0
+        finally:
+            os.environ.pop("WSE_CHUNK_BATCH", None)
+
+    log(f"prefill {n_prompt} tokens in {chunk}-token chunks, one launch per chunk and op")
+    dt_1 = None if batched_only else timed_prefill(False)
+    log(f"prefill {n_prompt} tokens in {chunk}-token chunks, the full chunks batched per op")
+    dt_p = timed_prefill(True)
     # FLOPs: every layer GEMM on every token (2 per weight), the causal
     # attention (q.k and p.v: 2 * 2 * head_dim per (head, cached position)),
     # and the head on the last token only.
@@ -377,6 +393,11 @@ def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False, gemms: bool = True,
                                f"then {n_new} greedy decode steps",
                    "prefill_ms": round(dt_p * 1e3, 2),
                    "prefill_tflops": round(flops / dt_p / 1e12, 2),
+                   "batched": "each layer's op runs for all 16 chunks in one launch, every "
+                              "launch with one chunk's tiling and split-K plan (bit-identical "
+                              "to one launch per chunk)",
+                   "prefill_tok_s_one_launch_per_chunk": round(n_prompt / dt_1, 1) if dt_1 else None,
+                   "prefill_ms_one_launch_per_chunk": round(dt_1 * 1e3, 2) if dt_1 else None,
                    "prefill_flops": flops,
                    "decode_steps": n_new,
                    "decode_tok_s": round(n_new / dt_d, 1) if dt_d else None,
@@ -438,6 +459,7 @@ def secondary_configs(E, wk) -> dict:
     c = p["config"]
     out["config4"] = {"workload": c["workload"], "prefill_tok_s": p["value"],
                       "prefill_ms": c["prefill_ms"], "prefill_tflops": c["prefill_tflops"],
+                      "prefill_tok_s_one_launch_per_chunk": c["prefill_tok_s_one_launch_per_chunk"],
                       "decode_tok_s": c["decode_tok_s"]}
     log("secondary: config 1 (lm_head GEMV 896 -> 151936, weights cold)")
     h = gemv_bench(wk, 200, head_only=True, emit=False)["config"]["shapes"]["lm_head"]
@@ -716,7 +738,7 @@ def main():
         gemv_bench(wk, max(a.steps, 200))
         return
     if a.config == 4:
-        prefill_bench(E, wk, a.steps, a.gemm_7b)
+        prefill_bench(E, wk, a.steps, a.gemm_7b, batched_only=a.batched_only)
         return
     if a.floors:
         floors_bench(E, wk, a.config, max(a.steps, 20))

@@ -187,6 +187,30 @@ wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si, const void
                                       int32_t max_seq, const void *q_norm_w,
                                       const void *k_norm_w, float eps);
 
+/* The same four chunk GEMM forms (and the plain one) over n tokens that hold
+ * several chunks, with the tiling and split-K plan of a plan_n-token chunk
+ * repeated over the n tokens: each token gets the bits a call of plan_n
+ * tokens gives it (n = plan_n is the call above). The batched prefill uses
+ * them to run a layer's op for every full chunk in one launch. */
+wst_status_t wst_gemm_int4_hier_chunks(const void *qw, const void *si, const void *sb,
+                                       const void *x, const void *bias, void *y, int32_t in_f,
+                                       int32_t out_f, int32_t n, int32_t accum, int32_t plan_n);
+wst_status_t wst_gemm_hier_swiglu_chunks(const void *qw, const void *si, const void *sb,
+                                         const void *x, void *act, int32_t in_f, int32_t inter,
+                                         int32_t n, int32_t plan_n);
+wst_status_t wst_gemm_hier_norm_chunks(const void *qw, const void *si, const void *sb,
+                                       const void *x, const void *bias, void *y, int32_t in_f,
+                                       int32_t out_f, int32_t n, int32_t accum,
+                                       const void *norm_w, float eps, void *h_out,
+                                       int32_t plan_n);
+wst_status_t wst_gemm_hier_rope_chunks(const void *qw, const void *si, const void *sb,
+                                       const void *x, const void *bias, void *qkv, int32_t in_f,
+                                       void *k_cache, void *v_cache, const void *cos_tab,
+                                       const void *sin_tab, int32_t n_q, int32_t n_kv,
+                                       int32_t head_dim, int32_t pos0, int32_t n,
+                                       int32_t max_seq, const void *q_norm_w,
+                                       const void *k_norm_w, float eps, int32_t plan_n);
+
 /* ------------------------------------------------------------ measurement */
 
 /* One launch of the library's streaming-read kernel (16-byte nontemporal

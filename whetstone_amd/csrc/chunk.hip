@@ -13,21 +13,30 @@ extern "C" int32_t wst_chunk_max_tokens(void) { return CHUNK_MAX_TOKENS; }
 // Implemented in gemm.hip (MFMA).
 wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void *sb,
                            const void *x, const void *bias, void *y, int32_t in_f, int32_t out_f,
-                           int32_t n, int32_t accum, float *ws_ext = nullptr, size_t ws_cap = 0);
+                           int32_t n, int32_t accum, float *ws_ext = nullptr, size_t ws_cap = 0,
+                           int32_t plan_n = 0);
 
-extern "C" wst_status_t wst_gemm_int4_hier(const void *qw, const void *si, const void *sb,
-                                           const void *x, const void *bias, void *y,
-                                           int32_t in_f, int32_t out_f, int32_t n,
-                                           int32_t accum) {
+extern "C" wst_status_t wst_gemm_int4_hier_chunks(const void *qw, const void *si, const void *sb,
+                                                  const void *x, const void *bias, void *y,
+                                                  int32_t in_f, int32_t out_f, int32_t n,
+                                                  int32_t accum, int32_t plan_n) {
   WST_REQUIRE(qw && si && sb && x && y, "wst_gemm_int4_hier: null pointer");
   WST_REQUIRE(in_f > 0 && out_f > 0 && n > 0, "wst_gemm_int4_hier: non-positive dimension");
   WST_REQUIRE(in_f % 32 == 0, "wst_gemm_int4_hier: in_features must be a multiple of 32");
   WST_REQUIRE(!(((uintptr_t)qw | (uintptr_t)x) & 15u),
               "wst_gemm_int4_hier: qw and x must be 16-byte aligned");
-  const wst_status_t st = wst_gemm_mfma(true, qw, si, sb, x, bias, y, in_f, out_f, n, accum);
+  const wst_status_t st =
+      wst_gemm_mfma(true, qw, si, sb, x, bias, y, in_f, out_f, n, accum, nullptr, 0, plan_n);
   if (st != WST_OK) return st;
   WST_TRY_KERNEL("wst_gemm_int4_hier");
   return WST_OK;
+}
+
+extern "C" wst_status_t wst_gemm_int4_hier(const void *qw, const void *si, const void *sb,
+                                           const void *x, const void *bias, void *y,
+                                           int32_t in_f, int32_t out_f, int32_t n,
+                                           int32_t accum) {
+  return wst_gemm_int4_hier_chunks(qw, si, sb, x, bias, y, in_f, out_f, n, accum, n);
 }
 
 extern "C" wst_status_t wst_gemm_fp16(const void *w, const void *x, const void *bias, void *y,
@@ -171,7 +180,11 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
     int pos0, int n, int max_seq, float scale) {
   using S = AcShape<HD>;
   extern __shared__ __align__(16) uint16_t ac_lds[];
-  const int head = blockIdx.x, t0 = blockIdx.y * AC_TT;
+  // Token groups in reverse order: blocks are dispatched in index order, and
+  // the last tokens attend to the most positions, so the longest blocks start
+  // first and the short ones fill in behind them (a batched prefill's causal
+  // work spans 16x between its first and last chunk).
+  const int head = blockIdx.x, t0 = (gridDim.y - 1 - blockIdx.y) * AC_TT;
   const int kvh = head / (n_q / n_kv);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the tile loop is scalar

@@ -61,6 +61,10 @@ struct wse_engine {
   void *c_tokens = nullptr, *c_x = nullptr, *c_h = nullptr, *c_qkv = nullptr, *c_attn = nullptr,
        *c_act = nullptr;
   void *c_logits = nullptr, *c_picks = nullptr;  // the chunk head's, on first use
+  // Buffers of a prefill whose full chunks share their launches (b_cap tokens).
+  int b_cap = 0;
+  void *b_tokens = nullptr, *b_x = nullptr, *b_h = nullptr, *b_qkv = nullptr,
+       *b_attn = nullptr, *b_act = nullptr;
   void *nll_acc = nullptr;                       // cross_entropy's (sum, count), on first use
   std::deque<int32_t> recent;                    // repetition-penalty window (RECENT_CAP)
   bool c_ran = false;                            // a chunk pass has left picks
@@ -891,11 +895,24 @@ static wst_status_t ensure_chunk_head(wse_engine *e) {
   return WST_OK;
 }
 
+struct ChunkBufs {
+  void *tokens, *x, *h, *qkv, *attn, *act;
+};
+
 // Engine::forward_chunk_ex (engine.rs:748-844). With want_logits the final
-// norm and the head (a plain chunk GEMM: no rescore) run for every row, the
-// chunk argmax leaves each row's greedy pick, and the last row's logits and
-// pick are copied to the single-token buffers (logits, token cursor).
-static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool want_logits) {
+// norm and the head (a plain chunk GEMM: no rescore) run for every row of the
+// last chunk, the chunk argmax leaves each of those rows' greedy pick, and the
+// last row's logits and pick are copied to the single-token buffers (logits,
+// token cursor).
+//
+// n tokens in chunks of `width`: with n > width the chunks go through each
+// layer together, one launch per op for all of them (the batched prefill),
+// every launch keeping one chunk's tiling and split-K plan (plan_n = width),
+// so that every token gets the bits the chunk-by-chunk pass gives it. A
+// chunk's attention reads the cache only up to its own last position, so the
+// later chunks' K/V rows already in the cache are never read.
+static wst_status_t chunk_pass(wse_engine *e, const int32_t *ids, int n, bool want_logits,
+                               int width, const ChunkBufs &b) {
   const wse_model &m = *e->m;
   const wse_config_t &c = m.c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_q, nkv = c.n_kv, I = c.inter, V = c.vocab;
@@ -907,62 +924,96 @@ static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool
     return WST_ERR_SHAPE;
   }
   const int pos0 = e->pos;
-  TRY(wst_memcpy_h2d(e->c_tokens, ids, (size_t)n * 4));
+  const int pn = width < n ? width : n;  // the plan's token count
+  TRY(wst_memcpy_h2d(b.tokens, ids, (size_t)n * 4));
   if (m.embed.dense())
-    TRY(wst_embed_fp16_chunk(m.embed.w16, e->c_tokens, e->c_x, H, V, n));
+    TRY(wst_embed_fp16_chunk(m.embed.w16, b.tokens, b.x, H, V, n));
   else
-    TRY(wst_embed_int4_hier_chunk(m.embed.qw, m.embed.si, m.embed.sb, e->c_tokens, e->c_x, H, V,
-                                  n));
+    TRY(wst_embed_int4_hier_chunk(m.embed.qw, m.embed.si, m.embed.sb, b.tokens, b.x, H, V, n));
   // Fused chunk forms (whetstone_ext.h; bit-identical to the reference's op
   // sequence): qkv GEMM + RoPE/KV append, o GEMM + post-attention norm, gate|up
   // GEMM + SwiGLU, down GEMM + the next norm (the next layer's input norm, or
   // the final norm before the head). Unfused where a fused form does not
   // apply (f16 head path aside, head_dim above 128).
   const bool rope_fused = hd <= 128;
-  TRY(wst_rmsnorm_chunk(e->c_x, m.layers[0].in_norm, e->c_h, H, n, eps));
+  TRY(wst_rmsnorm_chunk(b.x, m.layers[0].in_norm, b.h, H, n, eps));
   for (int l = 0; l < c.n_layers; ++l) {
     const Layer &L = m.layers[(size_t)l];
     if (rope_fused) {
-      TRY(wst_gemm_hier_rope_chunk(L.qkv.qw, L.qkv.si, L.qkv.sb, e->c_h, L.qkv_bias, e->c_qkv, H,
-                                   e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab, e->sin_tab, nq,
-                                   nkv, hd, pos0, n, e->max_seq, L.q_norm, L.k_norm, eps));
+      TRY(wst_gemm_hier_rope_chunks(L.qkv.qw, L.qkv.si, L.qkv.sb, b.h, L.qkv_bias, b.qkv, H,
+                                    e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab, e->sin_tab,
+                                    nq, nkv, hd, pos0, n, e->max_seq, L.q_norm, L.k_norm, eps,
+                                    pn));
     } else {
-      TRY(wst_gemm_int4_hier(L.qkv.qw, L.qkv.si, L.qkv.sb, e->c_h, L.qkv_bias, e->c_qkv, H, nqkv,
-                             n, 0));
-      TRY(wst_rope_cache_chunk(e->c_qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab,
+      TRY(wst_gemm_int4_hier_chunks(L.qkv.qw, L.qkv.si, L.qkv.sb, b.h, L.qkv_bias, b.qkv, H, nqkv,
+                                    n, 0, pn));
+      TRY(wst_rope_cache_chunk(b.qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->cos_tab,
                                e->sin_tab, nq, nkv, hd, pos0, n, e->max_seq, L.q_norm, L.k_norm,
                                eps));
     }
-    TRY(wst_attn_chunk(e->c_qkv, e->kc[(size_t)l], e->vc[(size_t)l], e->c_attn, nq, nkv, hd, pos0,
-                       n, e->max_seq, scale));
-    TRY(wst_gemm_hier_norm_chunk(L.o.qw, L.o.si, L.o.sb, e->c_attn, nullptr, e->c_x, nq * hd, H, n,
-                                 1, L.post_norm, eps, e->c_h));
-    TRY(wst_gemm_hier_swiglu_chunk(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, e->c_h, e->c_act, H,
-                                   I, n));
+    TRY(wst_attn_chunk(b.qkv, e->kc[(size_t)l], e->vc[(size_t)l], b.attn, nq, nkv, hd, pos0, n,
+                       e->max_seq, scale));
+    TRY(wst_gemm_hier_norm_chunks(L.o.qw, L.o.si, L.o.sb, b.attn, nullptr, b.x, nq * hd, H, n, 1,
+                                  L.post_norm, eps, b.h, pn));
+    TRY(wst_gemm_hier_swiglu_chunks(L.gate_up.qw, L.gate_up.si, L.gate_up.sb, b.h, b.act, H, I,
+                                    n, pn));
     const bool last = l + 1 == c.n_layers;
     if (!last || want_logits)
-      TRY(wst_gemm_hier_norm_chunk(L.down.qw, L.down.si, L.down.sb, e->c_act, nullptr, e->c_x, I,
-                                   H, n, 1, last ? m.final_norm : m.layers[(size_t)l + 1].in_norm,
-                                   eps, e->c_h));
+      TRY(wst_gemm_hier_norm_chunks(L.down.qw, L.down.si, L.down.sb, b.act, nullptr, b.x, I, H, n,
+                                    1, last ? m.final_norm : m.layers[(size_t)l + 1].in_norm, eps,
+                                    b.h, pn));
     else
-      TRY(wst_gemm_int4_hier(L.down.qw, L.down.si, L.down.sb, e->c_act, nullptr, e->c_x, I, H, n,
-                             1));
+      TRY(wst_gemm_int4_hier_chunks(L.down.qw, L.down.si, L.down.sb, b.act, nullptr, b.x, I, H, n,
+                                    1, pn));
   }
   if (want_logits) {
+    // the last chunk's rows
+    const int r0 = (n - 1) / pn * pn, nr = n - r0;
+    const void *hl = (const char *)b.h + (size_t)r0 * H * 2;
     const Mat &head = m.head();
     TRY(ensure_chunk_head(e));
     if (head.dense())
-      TRY(wst_gemm_fp16(head.w16, e->c_h, nullptr, e->c_logits, H, V, n, 0));
+      TRY(wst_gemm_fp16(head.w16, hl, nullptr, e->c_logits, H, V, nr, 0));
     else
-      TRY(wst_gemm_int4_hier(head.qw, head.si, head.sb, e->c_h, nullptr, e->c_logits, H, V, n, 0));
-    TRY(wst_argmax_chunk(e->c_logits, e->c_picks, V, n));
-    TRY(wst_memcpy_d2d(e->logits, (const char *)e->c_logits + (size_t)(n - 1) * V * 4,
+      TRY(wst_gemm_int4_hier(head.qw, head.si, head.sb, hl, nullptr, e->c_logits, H, V, nr, 0));
+    TRY(wst_argmax_chunk(e->c_logits, e->c_picks, V, nr));
+    TRY(wst_memcpy_d2d(e->logits, (const char *)e->c_logits + (size_t)(nr - 1) * V * 4,
                        (size_t)V * 4));
-    TRY(wst_memcpy_d2d(e->token, (const char *)e->c_picks + (size_t)(n - 1) * 4, 4));
+    TRY(wst_memcpy_d2d(e->token, (const char *)e->c_picks + (size_t)(nr - 1) * 4, 4));
     e->c_ran = true;
   }
   for (int i = 0; i < n; ++i) note(e, ids[i]);
   return wse_engine_set_pos(e, pos0 + n);
+}
+
+static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool want_logits) {
+  const ChunkBufs b{e->c_tokens, e->c_x, e->c_h, e->c_qkv, e->c_attn, e->c_act};
+  return chunk_pass(e, ids, n, want_logits, e->chunk_width, b);
+}
+
+// The batched prefill's buffers, grown to n tokens.
+static wst_status_t ensure_batch(wse_engine *e, int n) {
+  if (e->b_cap >= n) return WST_OK;
+  const wse_config_t &c = e->m->c;
+  const size_t w = (size_t)n;
+  const size_t H = (size_t)c.hidden, hd = (size_t)c.head_dim, I = (size_t)c.inter;
+  const size_t nqkv = (size_t)(c.n_q + 2 * c.n_kv) * hd;
+  Arena &a = e->arena;
+  TRY(a.alloc(&e->b_tokens, w * 4, true));
+  TRY(a.alloc(&e->b_x, w * H * 4, true));
+  TRY(a.alloc(&e->b_h, w * H * 2, true));
+  TRY(a.alloc(&e->b_qkv, w * nqkv * 4, true));
+  TRY(a.alloc(&e->b_attn, w * (size_t)c.n_q * hd * 2, true));
+  TRY(a.alloc(&e->b_act, w * I * 2, true));
+  e->b_cap = n;
+  return WST_OK;
+}
+
+// The full chunks of a chunked prefill go through each layer together
+// (chunk_pass with n > width); WSE_CHUNK_BATCH=0 runs them one by one.
+static bool chunk_batch_on() {
+  const char *v = getenv("WSE_CHUNK_BATCH");
+  return !(v && v[0] == '0');
 }
 
 wst_status_t wse_engine_max_seq(const wse_engine_t *e, int32_t *out) {
@@ -1024,7 +1075,15 @@ wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids, int32_t n, 
   if (chunked && n > 1) {
     TRY(ensure_chunk(e));
     const int w = e->chunk_width;
-    for (int s = 0; s < n; s += w) {
+    int s = 0;
+    const int full = n / w * w;  // the full chunks (a shorter last chunk keeps its own plan)
+    if (chunk_batch_on() && full >= 2 * w) {
+      TRY(ensure_batch(e, full));
+      const ChunkBufs b{e->b_tokens, e->b_x, e->b_h, e->b_qkv, e->b_attn, e->b_act};
+      TRY(chunk_pass(e, ids, full, full == n, w, b));
+      s = full;
+    }
+    for (; s < n; s += w) {
       const int k = n - s < w ? n - s : w;
       TRY(forward_chunk(e, ids + s, k, s + k == n));
     }

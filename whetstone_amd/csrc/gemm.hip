@@ -853,9 +853,16 @@ static int gemm_bn_override() {
 // with in_f picks the tiles: the wide tiles for long rows or many of them,
 // where their deeper pipeline pays; short K with few rows (the 0.5B qkv and
 // o projections) splits K into pieces too short for it.
-GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0, bool swi = false) {
+// plan_n: the token count whose tiling and split-K plan the launch uses; n
+// may exceed it (several chunks in one launch): the grid then repeats the
+// plan's token tiles over n, and every token gets the bits a launch of
+// plan_n tokens gives it (the tiles are 64, 128 or 256 tokens, which divide
+// a chunk). 0: n itself.
+GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0, bool swi = false,
+                   int plan_n = 0) {
   GemmPlan p;
   if (rows <= 0) rows = out_f;
+  const int pn = plan_n > 0 && plan_n < n ? plan_n : n;
   // (The wide tiles address x with 32-bit byte offsets.)
   p.wide = hier && wide_tiles() && in_f >= GW_KC && (in_f >= 2048 || rows >= 4096) &&
            (size_t)n * in_f * 2 < ((size_t)1 << 31);
@@ -867,14 +874,14 @@ GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0, b
   p.nwv = 8;
   if (p.wide) {
     const int forced = gemm_bn_override();
-    const int t256 = ((out_f + GW_BM - 1) / GW_BM) * ((n + 255) / 256);
-    if (forced == 128 || (forced != 256 && !swi && n > 128 && t256 < wst_cu_count())) p.nwv = 4;
+    const int t256 = ((out_f + GW_BM - 1) / GW_BM) * ((pn + 255) / 256);
+    if (forced == 128 || (forced != 256 && !swi && pn > 128 && t256 < wst_cu_count())) p.nwv = 4;
   }
   p.bm = p.wide ? GW_BM : GM_BM;
   p.bn = p.wide ? 32 * p.nwv : GM_BN;
   p.kg = p.wide ? GW_KG : GM_KG;
   const int G = in_f / HGROUP;
-  const int tiles = ((out_f + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
+  const int tiles = ((out_f + p.bm - 1) / p.bm) * ((pn + p.bn - 1) / p.bn);
   p.splits = 1;
   p.gps = G;
   const int target = wst_cu_count();
@@ -917,8 +924,9 @@ void launch_gemm(const GemmPlan &p, const void *w, const void *si, const void *s
 // The GEMM into the split scratch (always, even with one split): the fused
 // reduce kernels read it.
 wst_status_t gemm_to_scratch(const void *w, const void *si, const void *sb, const void *x,
-                             int in_f, int out_f, int n, float **ws_out, int *splits_out) {
-  const GemmPlan p = plan_gemm(in_f, out_f, n);
+                             int in_f, int out_f, int n, float **ws_out, int *splits_out,
+                             int plan_n = 0) {
+  const GemmPlan p = plan_gemm(in_f, out_f, n, true, 0, false, plan_n);
   float *ws = (float *)wst_static_scratch(WST_SCRATCH_GEMM, (size_t)p.splits * n * out_f * 4);
   if (!ws) return WST_ERR_OOM;
   launch_gemm<true, false>(p, w, si, sb, x, nullptr, nullptr, ws, in_f, out_f, n, 0);
@@ -932,8 +940,9 @@ wst_status_t gemm_to_scratch(const void *w, const void *si, const void *sb, cons
 // of the library's lazily grown scratch slot, and nothing is allocated.
 wst_status_t wst_gemm_mfma(bool hier, const void *w, const void *si, const void *sb,
                            const void *x, const void *bias, void *y, int32_t in_f, int32_t out_f,
-                           int32_t n, int32_t accum, float *ws_ext, size_t ws_cap) {
-  const GemmPlan p = plan_gemm(in_f, out_f, n, hier);
+                           int32_t n, int32_t accum, float *ws_ext, size_t ws_cap,
+                           int32_t plan_n) {
+  const GemmPlan p = plan_gemm(in_f, out_f, n, hier, 0, false, plan_n);
   const int splits = p.splits;
   float *ws = nullptr;
   if (splits > 1) {
@@ -980,14 +989,15 @@ static wst_status_t chunk_gemm_args(const void *qw, const void *si, const void *
   return WST_OK;
 }
 
-extern "C" wst_status_t wst_gemm_hier_swiglu_chunk(const void *qw, const void *si,
-                                                   const void *sb, const void *x, void *act,
-                                                   int32_t in_f, int32_t inter, int32_t n) {
+extern "C" wst_status_t wst_gemm_hier_swiglu_chunks(const void *qw, const void *si,
+                                                    const void *sb, const void *x, void *act,
+                                                    int32_t in_f, int32_t inter, int32_t n,
+                                                    int32_t plan_n) {
   wst_status_t st = chunk_gemm_args(qw, si, sb, x, in_f, inter, n, "wst_gemm_hier_swiglu_chunk");
   if (st != WST_OK) return st;
   WST_REQUIRE(act, "wst_gemm_hier_swiglu_chunk: null pointer");
   // Never split: a tile pairs BM/2 gate rows with the matching up rows.
-  GemmPlan p = plan_gemm(in_f, inter, n, true, 2 * inter, true);
+  GemmPlan p = plan_gemm(in_f, inter, n, true, 2 * inter, true, plan_n);
   p.splits = 1;
   p.gps = in_f / HGROUP;
   p.grid = dim3((inter + p.bm / 2 - 1) / (p.bm / 2), (n + p.bn - 1) / p.bn, 1);
@@ -996,18 +1006,24 @@ extern "C" wst_status_t wst_gemm_hier_swiglu_chunk(const void *qw, const void *s
   return WST_OK;
 }
 
-extern "C" wst_status_t wst_gemm_hier_norm_chunk(const void *qw, const void *si, const void *sb,
-                                                const void *x, const void *bias, void *y,
-                                                int32_t in_f, int32_t out_f, int32_t n,
-                                                int32_t accum, const void *norm_w, float eps,
-                                                void *h_out) {
+extern "C" wst_status_t wst_gemm_hier_swiglu_chunk(const void *qw, const void *si,
+                                                   const void *sb, const void *x, void *act,
+                                                   int32_t in_f, int32_t inter, int32_t n) {
+  return wst_gemm_hier_swiglu_chunks(qw, si, sb, x, act, in_f, inter, n, n);
+}
+
+extern "C" wst_status_t wst_gemm_hier_norm_chunks(const void *qw, const void *si, const void *sb,
+                                                 const void *x, const void *bias, void *y,
+                                                 int32_t in_f, int32_t out_f, int32_t n,
+                                                 int32_t accum, const void *norm_w, float eps,
+                                                 void *h_out, int32_t plan_n) {
   wst_status_t st = chunk_gemm_args(qw, si, sb, x, in_f, out_f, n, "wst_gemm_hier_norm_chunk");
   if (st != WST_OK) return st;
   WST_REQUIRE(y && norm_w && h_out, "wst_gemm_hier_norm_chunk: null pointer");
   WST_REQUIRE(out_f <= 16384, "wst_gemm_hier_norm_chunk: out_features above 16384");
   float *ws;
   int splits;
-  st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits);
+  st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits, plan_n);
   if (st != WST_OK) return st;
   static bool attr = false;
   if (!attr) {
@@ -1026,14 +1042,23 @@ extern "C" wst_status_t wst_gemm_hier_norm_chunk(const void *qw, const void *si,
   return WST_OK;
 }
 
-extern "C" wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si, const void *sb,
-                                                const void *x, const void *bias, void *qkv,
-                                                int32_t in_f, void *k_cache, void *v_cache,
-                                                const void *cos_tab, const void *sin_tab,
-                                                int32_t n_q, int32_t n_kv, int32_t head_dim,
-                                                int32_t pos0, int32_t n, int32_t max_seq,
-                                                const void *q_norm_w, const void *k_norm_w,
-                                                float eps) {
+extern "C" wst_status_t wst_gemm_hier_norm_chunk(const void *qw, const void *si, const void *sb,
+                                                const void *x, const void *bias, void *y,
+                                                int32_t in_f, int32_t out_f, int32_t n,
+                                                int32_t accum, const void *norm_w, float eps,
+                                                void *h_out) {
+  return wst_gemm_hier_norm_chunks(qw, si, sb, x, bias, y, in_f, out_f, n, accum, norm_w, eps,
+                                   h_out, n);
+}
+
+extern "C" wst_status_t wst_gemm_hier_rope_chunks(const void *qw, const void *si, const void *sb,
+                                                 const void *x, const void *bias, void *qkv,
+                                                 int32_t in_f, void *k_cache, void *v_cache,
+                                                 const void *cos_tab, const void *sin_tab,
+                                                 int32_t n_q, int32_t n_kv, int32_t head_dim,
+                                                 int32_t pos0, int32_t n, int32_t max_seq,
+                                                 const void *q_norm_w, const void *k_norm_w,
+                                                 float eps, int32_t plan_n) {
   WST_REQUIRE(n_q > 0 && n_kv > 0 && head_dim > 0 && n > 0 && n <= 65535,
               "wst_gemm_hier_rope_chunk: bad shape");
   WST_REQUIRE(head_dim % 2 == 0 && head_dim <= 128, "wst_gemm_hier_rope_chunk: head_dim above 128");
@@ -1046,7 +1071,7 @@ extern "C" wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si,
               "wst_gemm_hier_rope_chunk: chunk does not fit the cache");
   float *ws;
   int splits;
-  st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits);
+  st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits, plan_n);
   if (st != WST_OK) return st;
   gemm_reduce_rope_kernel<<<dim3(n_q + n_kv, n), 64, 0, WST_STREAM>>>(
       ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,
@@ -1054,6 +1079,19 @@ extern "C" wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si,
       pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
   WST_TRY_KERNEL("wst_gemm_hier_rope_chunk");
   return WST_OK;
+}
+
+extern "C" wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si, const void *sb,
+                                                const void *x, const void *bias, void *qkv,
+                                                int32_t in_f, void *k_cache, void *v_cache,
+                                                const void *cos_tab, const void *sin_tab,
+                                                int32_t n_q, int32_t n_kv, int32_t head_dim,
+                                                int32_t pos0, int32_t n, int32_t max_seq,
+                                                const void *q_norm_w, const void *k_norm_w,
+                                                float eps) {
+  return wst_gemm_hier_rope_chunks(qw, si, sb, x, bias, qkv, in_f, k_cache, v_cache, cos_tab,
+                                   sin_tab, n_q, n_kv, head_dim, pos0, n, max_seq, q_norm_w,
+                                   k_norm_w, eps, n);
 }
 
 // ------------------------------------------- the no-allocation GEMM entry
@@ -1105,7 +1143,7 @@ extern "C" wst_status_t wst_gemm_int4_hier_noalloc(const void *qw, const void *s
   float *ws = noalloc_scratch();
   if (!ws) return WST_ERR_CUDA;
   const wst_status_t st =
-      wst_gemm_mfma(true, qw, si, sb, x, bias, y, in_f, out_f, n, accum, ws, GM_NOALLOC_BYTES);
+      wst_gemm_mfma(true, qw, si, sb, x, bias, y, in_f, out_f, n, accum, ws, GM_NOALLOC_BYTES, 0);
   if (st != WST_OK) return st;
   WST_TRY_KERNEL("wst_gemm_int4_hier_noalloc");
   return WST_OK;
