@@ -330,9 +330,9 @@ def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False, gemms: bool = True,
     eng = E.Engine(g, n_prompt + n_new + 8)
     ids = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt).astype(np.int32)
     def timed_prefill(batch: bool) -> float:
-        # The full chunks share each layer's launches unless batch is off
-        # (WSE_CHUNK_BATCH=0: one launch per chunk and op); the bits are the
-        # same either way. A warm-up prefill first (kernels, buffers, split
+        # The full chunks share each layer's launches, each planned for all
+        # its tokens, unless batch is off (WSE_CHUNK_BATCH=0: one launch per
+        # chunk and op). A warm-up prefill first (kernels, buffers, split
         # scratch), then rewind.
         os.environ["WSE_CHUNK_BATCH"] = "1" if batch else "0"
         try:

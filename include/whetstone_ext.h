@@ -190,8 +190,9 @@ wst_status_t wst_gemm_hier_rope_chunk(const void *qw, const void *si, const void
 /* The same four chunk GEMM forms (and the plain one) over n tokens that hold
  * several chunks, with the tiling and split-K plan of a plan_n-token chunk
  * repeated over the n tokens: each token gets the bits a call of plan_n
- * tokens gives it (n = plan_n is the call above). The batched prefill uses
- * them to run a layer's op for every full chunk in one launch. */
+ * tokens gives it (n = plan_n is the call above); plan_n = 0 plans for the
+ * n tokens themselves. The batched prefill uses them to run a layer's op for
+ * every full chunk in one launch. */
 wst_status_t wst_gemm_int4_hier_chunks(const void *qw, const void *si, const void *sb,
                                        const void *x, const void *bias, void *y, int32_t in_f,
                                        int32_t out_f, int32_t n, int32_t accum, int32_t plan_n);

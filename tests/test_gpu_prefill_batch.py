@@ -1,11 +1,19 @@
 """The batched prefill against the chunk-by-chunk one.
 
 A chunked prefill's full chunks go through each layer together, one launch
-per op for all of them (engine.cpp chunk_pass), each launch keeping one
-chunk's tiling and split-K plan. The contract is bit-identity with running
-the same chunks one after the other (WSE_CHUNK_BATCH=0): the last chunk's
-logits, its greedy picks, every KV-cache row (seen through the decode steps
-that follow), and the greedy stream after the prompt.
+per op for all of them (engine.cpp chunk_pass).
+
+* WSE_CHUNK_BATCH=chunk: each launch keeps one chunk's tiling and split-K
+  plan. The contract is bit-identity with running the same chunks one after
+  the other (WSE_CHUNK_BATCH=0): the last chunk's logits, its greedy picks,
+  every KV-cache row (seen through the decode steps that follow), and the
+  greedy stream after the prompt.
+* the default: each launch is planned for all its tokens, which drops the
+  split-K one chunk's few tiles need, so a GEMM's K sum runs in one pass
+  instead of split partials added afterwards. Only the f32 summation order
+  changes: the logits stay within the north star's tolerance of the
+  chunk-by-chunk ones, and the greedy picks and stream are identical except
+  where a top-2 margin is below twice their distance.
 """
 import os
 
@@ -16,9 +24,13 @@ from whetstone_amd import engine as E
 
 pytestmark = pytest.mark.gpu
 
+CFGS = {"05b_qk_rescore": dict(E.QWEN05B, qk_norm=1, rescore_k=32), "05b": E.QWEN05B,
+        "7b": dict(E.QWEN7B, n_layers=4)}
+CASES = [("05b_qk_rescore", 1024), ("05b_qk_rescore", 900), ("05b", 768), ("7b", 512)]
 
-def _run(g, prompt, n_new, batch):
-    os.environ["WSE_CHUNK_BATCH"] = "1" if batch else "0"
+
+def _run(g, prompt, n_new, mode):
+    os.environ["WSE_CHUNK_BATCH"] = mode
     try:
         eng = E.Engine(g, len(prompt) + n_new + 8)
         assert eng.chunk_width() == 256
@@ -26,27 +38,66 @@ def _run(g, prompt, n_new, batch):
         logits = eng.logits().copy()
         tok = eng.token()
         picks = eng.chunk_picks(len(prompt) - (len(prompt) - 1) // 256 * 256)
-        toks = [tok]
+        toks, step_logits = [tok], [logits]
         for _ in range(n_new):
             eng.step()
             toks.append(eng.token())
+            step_logits.append(eng.logits().copy())
         eng.close()
     finally:
         os.environ.pop("WSE_CHUNK_BATCH", None)
-    return logits, picks, toks
+    return logits, picks, toks, step_logits
 
 
-@pytest.mark.parametrize("cfg_name,n_prompt", [("05b_qk_rescore", 1024), ("05b_qk_rescore", 900),
-                                               ("05b", 768), ("7b", 512)])
-def test_batched_prefill_is_bit_identical_to_chunk_by_chunk(cfg_name, n_prompt):
-    cfg = {"05b_qk_rescore": dict(E.QWEN05B, qk_norm=1, rescore_k=32), "05b": E.QWEN05B,
-           "7b": dict(E.QWEN7B, n_layers=4)}[cfg_name]
+def _setup(cfg_name, n_prompt):
+    cfg = CFGS[cfg_name]
     g = E.Model(cfg, seed=3)
     prompt = np.random.default_rng(n_prompt).integers(0, cfg["vocab"], n_prompt).astype(np.int32)
-    print(f"batched prefill: {cfg_name}, {n_prompt} tokens", flush=True)
-    a = _run(g, prompt, 8, False)
-    b = _run(g, prompt, 8, True)
+    return g, prompt
+
+
+@pytest.mark.parametrize("cfg_name,n_prompt", CASES)
+def test_batched_prefill_with_chunk_plans_is_bit_identical(cfg_name, n_prompt):
+    g, prompt = _setup(cfg_name, n_prompt)
+    print(f"batched prefill (chunk plans): {cfg_name}, {n_prompt} tokens", flush=True)
+    a = _run(g, prompt, 8, "0")
+    b = _run(g, prompt, 8, "chunk")
     g.close()
     assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32))
     assert np.array_equal(a[1], b[1])
     assert a[2] == b[2]
+
+
+def _top2(v):
+    s = np.sort(np.asarray(v, np.float64))
+    return float(s[-1] - s[-2])
+
+
+@pytest.mark.parametrize("cfg_name,n_prompt", CASES)
+def test_batched_prefill_planned_whole_matches_chunk_by_chunk(cfg_name, n_prompt):
+    g, prompt = _setup(cfg_name, n_prompt)
+    print(f"batched prefill (whole plans): {cfg_name}, {n_prompt} tokens", flush=True)
+    a = _run(g, prompt, 8, "0")
+    b = _run(g, prompt, 8, "1")
+    g.close()
+    d = float(np.max(np.abs(a[0].astype(np.float64) - b[0])))
+    scale = float(np.max(np.abs(a[0])))
+    print(f"  last-row logits: max-abs difference {d:.3g} (logits up to {scale:.3g})")
+    # an f32 reordering, not a different computation: within the north
+    # star's 1e-2 max-abs / 1e-3 relative (0.0030 measured at 24 layers; a
+    # dropped or doubled term moves the logits by O(1))
+    assert np.allclose(a[0], b[0], rtol=1e-3, atol=1e-2), d
+    # The last chunk's greedy picks: only its last row's logits are visible,
+    # so the other rows are held to 98% identical picks (a seeded model's
+    # top-2 margins over 151936 logits fall below 2d on about 1 row in 100).
+    same = np.asarray(a[1]) == np.asarray(b[1])
+    print(f"  last-chunk picks: {int(same.sum())}/{same.size} identical")
+    assert same[-1] or _top2(a[0]) < 2 * d
+    assert same.mean() >= 0.98, np.flatnonzero(~same)
+    # The greedy stream: identical up to a step whose top-2 margin is below
+    # twice that step's logit distance (the contexts agree up to there).
+    k = next((i for i, (x, y) in enumerate(zip(a[2], b[2])) if x != y), len(a[2]))
+    print(f"  greedy stream: {k}/{len(a[2])} tokens identical")
+    if k < len(a[2]):
+        dk = float(np.max(np.abs(a[3][k].astype(np.float64) - b[3][k])))
+        assert _top2(a[3][k]) < 2 * dk, (k, _top2(a[3][k]), dk)

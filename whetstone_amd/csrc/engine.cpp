@@ -906,13 +906,15 @@ struct ChunkBufs {
 // token cursor).
 //
 // n tokens in chunks of `width`: with n > width the chunks go through each
-// layer together, one launch per op for all of them (the batched prefill),
-// every launch keeping one chunk's tiling and split-K plan (plan_n = width),
-// so that every token gets the bits the chunk-by-chunk pass gives it. A
-// chunk's attention reads the cache only up to its own last position, so the
-// later chunks' K/V rows already in the cache are never read.
+// layer together, one launch per op for all of them (the batched prefill).
+// plan_n is the token count the GEMMs' tiling and split-K plan is made for:
+// n (plan_n = 0) lets a launch over many chunks drop the split-K that one
+// chunk's few tiles need; plan_n = width keeps one chunk's plan, so that every
+// token gets the bits the chunk-by-chunk pass gives it. A chunk's attention
+// reads the cache only up to its own last position, so the later chunks' K/V
+// rows already in the cache are never read.
 static wst_status_t chunk_pass(wse_engine *e, const int32_t *ids, int n, bool want_logits,
-                               int width, const ChunkBufs &b) {
+                               int width, int plan_n, const ChunkBufs &b) {
   const wse_model &m = *e->m;
   const wse_config_t &c = m.c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_q, nkv = c.n_kv, I = c.inter, V = c.vocab;
@@ -924,7 +926,7 @@ static wst_status_t chunk_pass(wse_engine *e, const int32_t *ids, int n, bool wa
     return WST_ERR_SHAPE;
   }
   const int pos0 = e->pos;
-  const int pn = width < n ? width : n;  // the plan's token count
+  const int pn = plan_n > 0 && plan_n < n ? plan_n : n;  // the plan's token count
   TRY(wst_memcpy_h2d(b.tokens, ids, (size_t)n * 4));
   if (m.embed.dense())
     TRY(wst_embed_fp16_chunk(m.embed.w16, b.tokens, b.x, H, V, n));
@@ -968,7 +970,7 @@ static wst_status_t chunk_pass(wse_engine *e, const int32_t *ids, int n, bool wa
   }
   if (want_logits) {
     // the last chunk's rows
-    const int r0 = (n - 1) / pn * pn, nr = n - r0;
+    const int r0 = (n - 1) / width * width, nr = n - r0;
     const void *hl = (const char *)b.h + (size_t)r0 * H * 2;
     const Mat &head = m.head();
     TRY(ensure_chunk_head(e));
@@ -988,7 +990,7 @@ static wst_status_t chunk_pass(wse_engine *e, const int32_t *ids, int n, bool wa
 
 static wst_status_t forward_chunk(wse_engine *e, const int32_t *ids, int n, bool want_logits) {
   const ChunkBufs b{e->c_tokens, e->c_x, e->c_h, e->c_qkv, e->c_attn, e->c_act};
-  return chunk_pass(e, ids, n, want_logits, e->chunk_width, b);
+  return chunk_pass(e, ids, n, want_logits, e->chunk_width, 0, b);
 }
 
 // The batched prefill's buffers, grown to n tokens.
@@ -1010,10 +1012,15 @@ static wst_status_t ensure_batch(wse_engine *e, int n) {
 }
 
 // The full chunks of a chunked prefill go through each layer together
-// (chunk_pass with n > width); WSE_CHUNK_BATCH=0 runs them one by one.
-static bool chunk_batch_on() {
+// (chunk_pass with n > width), planned for the whole launch (1, the default);
+// WSE_CHUNK_BATCH=chunk keeps one chunk's plan per launch (bit-identical to
+// the chunk-by-chunk pass); WSE_CHUNK_BATCH=0 runs the chunks one by one.
+enum BatchMode { BATCH_OFF, BATCH_WHOLE, BATCH_CHUNK_PLAN };
+static BatchMode chunk_batch_mode() {
   const char *v = getenv("WSE_CHUNK_BATCH");
-  return !(v && v[0] == '0');
+  if (!v || !v[0]) return BATCH_WHOLE;
+  if (v[0] == '0') return BATCH_OFF;
+  return strcmp(v, "chunk") == 0 ? BATCH_CHUNK_PLAN : BATCH_WHOLE;
 }
 
 wst_status_t wse_engine_max_seq(const wse_engine_t *e, int32_t *out) {
@@ -1077,10 +1084,11 @@ wst_status_t wse_engine_prefill(wse_engine_t *e, const int32_t *ids, int32_t n, 
     const int w = e->chunk_width;
     int s = 0;
     const int full = n / w * w;  // the full chunks (a shorter last chunk keeps its own plan)
-    if (chunk_batch_on() && full >= 2 * w) {
+    const BatchMode mode = chunk_batch_mode();
+    if (mode != BATCH_OFF && full >= 2 * w) {
       TRY(ensure_batch(e, full));
       const ChunkBufs b{e->b_tokens, e->b_x, e->b_h, e->b_qkv, e->b_attn, e->b_act};
-      TRY(chunk_pass(e, ids, full, full == n, w, b));
+      TRY(chunk_pass(e, ids, full, full == n, w, mode == BATCH_CHUNK_PLAN ? w : 0, b));
       s = full;
     }
     for (; s < n; s += w) {
