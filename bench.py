@@ -393,9 +393,9 @@ def prefill_bench(E, wk, n_new: int, gemm_7b: bool = False, gemms: bool = True,
                                f"then {n_new} greedy decode steps",
                    "prefill_ms": round(dt_p * 1e3, 2),
                    "prefill_tflops": round(flops / dt_p / 1e12, 2),
-                   "batched": "each layer's op runs for all 16 chunks in one launch, every "
-                              "launch with one chunk's tiling and split-K plan (bit-identical "
-                              "to one launch per chunk)",
+                   "batched": f"each layer's op runs for all {n_prompt // chunk} chunks in "
+                              "one launch, its GEMMs planned for all the tokens (f32 sums "
+                              "within rounding of one launch per chunk)",
                    "prefill_tok_s_one_launch_per_chunk": round(n_prompt / dt_1, 1) if dt_1 else None,
                    "prefill_ms_one_launch_per_chunk": round(dt_1 * 1e3, 2) if dt_1 else None,
                    "prefill_flops": flops,

@@ -6,6 +6,7 @@ the bit-exact checks this backend promises: unpack/embedding, argmax, the
 device packer, tile-rule independence, fused == unfused.
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -497,13 +498,27 @@ def test_gemm_fp16_matches_matmul(orc, wk, in_f, out_f, n):
     assert np.all(np.abs(got - want) <= bound)
 
 
+def _with_tg(tg, fn):
+    """Runs fn with the chunk attention's token groups per wave forced (1 or
+    2; None: the library's choice by token count)."""
+    if tg is None:
+        return fn()
+    os.environ["WST_ATTN_CHUNK_TG"] = str(tg)
+    try:
+        return fn()
+    finally:
+        os.environ.pop("WST_ATTN_CHUNK_TG", None)
+
+
+@pytest.mark.parametrize("tg", [1, 2])
 @pytest.mark.parametrize("n_q,n_kv,hd,pos0,n,max_seq", [
     (14, 2, 64, 0, 256, 256), (14, 2, 64, 1000, 44, 1100), (28, 4, 128, 0, 256, 300),
     (28, 4, 128, 3840, 256, 4096), (8, 8, 128, 5, 1, 16), (7, 1, 64, 2000, 37, 2100)])
 def test_chunk_attention_equals_per_token_decode_attention(orc, wk, n_q, n_kv, hd, pos0, n,
-                                                           max_seq):
+                                                           max_seq, tg):
     """Chunk attention (chunk_ops.cu:187-265) is decode attention per token:
-    token j attends to cache positions [0, pos0 + j] (chunk_kernels.rs:262-360)."""
+    token j attends to cache positions [0, pos0 + j] (chunk_kernels.rs:262-360).
+    Both token groupings of the MFMA kernel (16 or 32 tokens per block)."""
     rng = np.random.default_rng(pos0 + n + hd)
     kc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
     vc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
@@ -515,8 +530,8 @@ def test_chunk_attention_equals_per_token_decode_attention(orc, wk, n_q, n_kv, h
     qd = wk.DeviceBuffer.from_array(qkv)
     out = wk.DeviceBuffer(n * n_q * hd, np.float16)
     scale = np.float32(1.0 / math.sqrt(hd))
-    ffi.call("wst_attn_chunk", qd.ptr, cache.k.ptr, cache.v.ptr, out.ptr, n_q, n_kv, hd, pos0, n,
-             max_seq, scale)
+    _with_tg(tg, lambda: ffi.call("wst_attn_chunk", qd.ptr, cache.k.ptr, cache.v.ptr, out.ptr,
+                                  n_q, n_kv, hd, pos0, n, max_seq, scale))
     got = out.numpy().astype(np.float64).reshape(n, n_q * hd)
     for j in range(n):
         want = np.empty(n_q * hd, np.uint16)
@@ -525,11 +540,12 @@ def test_chunk_attention_equals_per_token_decode_attention(orc, wk, n_q, n_kv, h
         assert np.max(np.abs(got[j] - orc.f16_value(want))) < 2e-3, j
 
 
+@pytest.mark.parametrize("tg", [1, 2])
 @pytest.mark.parametrize("n_q,n_kv,hd,pos0,n,max_seq", [
     (14, 2, 64, 0, 256, 300), (28, 4, 128, 1000, 44, 1100), (14, 2, 64, 45, 256, 301),
     (28, 4, 128, 7, 20, 61)])
 def test_chunk_attention_ignores_nonfinite_past_the_attended_end(orc, wk, n_q, n_kv, hd, pos0,
-                                                                n, max_seq):
+                                                                n, max_seq, tg):
     """Cache positions at or past the chunk's last attended position hold NaN
     and Inf (inside the allocation): the output stays finite and equal to
     decode attention, so no tile reads them (a read would give 0 * NaN = NaN
@@ -552,12 +568,50 @@ def test_chunk_attention_ignores_nonfinite_past_the_attended_end(orc, wk, n_q, n
     out = wk.DeviceBuffer(n * n_q * hd, np.float16)
     scale = np.float32(1.0 / math.sqrt(hd))
     print(f"chunk attention with NaN/Inf past position {kend}: n_q {n_q} hd {hd} pos0 {pos0} "
-          f"n {n} max_seq {max_seq}", flush=True)
-    ffi.call("wst_attn_chunk", qd.ptr, cache.k.ptr, cache.v.ptr, out.ptr, n_q, n_kv, hd, pos0, n,
-             max_seq, scale)
+          f"n {n} max_seq {max_seq} tg {tg}", flush=True)
+    _with_tg(tg, lambda: ffi.call("wst_attn_chunk", qd.ptr, cache.k.ptr, cache.v.ptr, out.ptr,
+                                  n_q, n_kv, hd, pos0, n, max_seq, scale))
     got = out.numpy().astype(np.float64).reshape(n, n_q * hd)
     assert np.all(np.isfinite(got))
     for j in range(n):
+        want = np.empty(n_q * hd, np.uint16)
+        q = np.ascontiguousarray(qkv[j * row:j * row + n_q * hd])
+        orc.lib().orc_attn_decode(q, kc, vc, want, n_q, n_kv, hd, pos0 + j, max_seq, scale)
+        assert np.max(np.abs(got[j] - orc.f16_value(want))) < 2e-3, j
+
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,pos0,n", [(14, 2, 64, 0, 1536), (28, 4, 128, 300, 700),
+                                               (7, 1, 64, 33, 517)])
+def test_chunk_attention_token_groupings_are_bit_identical(orc, wk, n_q, n_kv, hd, pos0, n):
+    """A token's output does not depend on how many tokens share its block
+    (16 or 32): its valid keys are in the same tiles, taken by the same wave in
+    the same order, and a block's extra tiles are wholly masked for it. So the
+    library may pick the grouping by token count (a batched prefill and the
+    same chunks one by one get the same bits). Long prompts (the default picks
+    32 here) also checked against decode attention on a sample of tokens."""
+    max_seq = pos0 + n + 9
+    rng = np.random.default_rng(n + hd)
+    kc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
+    vc = f16(orc, rng.standard_normal(n_kv * max_seq * hd).astype(np.float32))
+    row = (n_q + 2 * n_kv) * hd
+    qkv = (rng.standard_normal(n * row) * 2).astype(np.float32)
+    cache = wk.KvCache(n_kv, n_q, hd, max_seq)
+    cache.k.copy_from(kc.view(np.float16))
+    cache.v.copy_from(vc.view(np.float16))
+    qd = wk.DeviceBuffer.from_array(qkv)
+    scale = np.float32(1.0 / math.sqrt(hd))
+    outs = {}
+    for tg in (1, 2, None):
+        out = wk.DeviceBuffer(n * n_q * hd, np.float16)
+        print(f"chunk attention tg {tg}: n_q {n_q} hd {hd} pos0 {pos0} n {n}", flush=True)
+        _with_tg(tg, lambda: ffi.call("wst_attn_chunk", qd.ptr, cache.k.ptr, cache.v.ptr,
+                                      out.ptr, n_q, n_kv, hd, pos0, n, max_seq, scale))
+        outs[tg] = out.numpy().view(np.uint16).copy()
+    assert np.array_equal(outs[1], outs[2]), int(np.sum(outs[1] != outs[2]))
+    assert np.array_equal(outs[None], outs[2])
+    got = outs[2].view(np.float16).astype(np.float64).reshape(n, n_q * hd)
+    for j in sorted({0, 1, 31, 32, n // 2, n - 33, n - 1}):
         want = np.empty(n_q * hd, np.uint16)
         q = np.ascontiguousarray(qkv[j * row:j * row + n_q * hd])
         orc.lib().orc_attn_decode(q, kc, vc, want, n_q, n_kv, hd, pos0 + j, max_seq, scale)

@@ -58,6 +58,11 @@ LIB_SOURCES = [
 ]
 ENGINE_SOURCES = ["engine.cpp", "wstone.cpp", "speculate.cpp", "sampler.cpp"]
 
+# Per-file code-generation flags. chunk.hip: MFMA accumulators in VGPRs (the
+# chunk attention's online softmax rescales and reads them between MFMAs; in
+# AGPRs each tile paid ~40 accvgpr moves).
+FILE_FLAGS = {"chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def hipcc() -> str:
     p = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -92,7 +97,8 @@ def build(verbose: bool = True, jobs: int | None = None) -> dict[str, Path]:
     eng_srcs = [CSRC / s for s in ENGINE_SOURCES if (CSRC / s).exists()]
     warnings: list[str] = []
     with cf.ThreadPoolExecutor(jobs) as ex:
-        futs = {ex.submit(_compile, s, OBJ / (s.stem + ".o"), []): s for s in lib_srcs + eng_srcs}
+        futs = {ex.submit(_compile, s, OBJ / (s.stem + ".o"), FILE_FLAGS.get(s.name, [])): s
+                for s in lib_srcs + eng_srcs}
         objs = {}
         for f in cf.as_completed(futs):
             obj, err = f.result()

@@ -124,86 +124,113 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
 // ------------------------------------------------------ MFMA chunk attention
 //
 // The same causal attention (chunk_ops.cu:187-265) as flash attention on
-// v_mfma_f32_16x16x32_f16, for head_dim 64 and 128:
-// * one 512-thread block per (query head, 16 query tokens); its eight waves
-//   take key tiles of 32 positions round-robin, each with its own online
-//   softmax, and merge once at the end through LDS;
-// * scores S = q . k^T: q (already rotated, times log2(e)/sqrt(hd), so the
-//   softmax is in base 2) enters as its f16 hi part plus the f16 rounding of
-//   the rest, so the products keep ~22 bits; K rows load coalesced (a
-//   128-byte row per eight lanes) into LDS, and the B operand (16 bytes of one
-//   position per lane) is read from there (loaded straight into that layout,
-//   each load touched sixteen part rows: hd 128 was 13% slower);
-// * P . V: P (hi + lo, as q) and V are turned into MFMA operands with the
-//   gfx950 transposing LDS read (ds_read_b64_tr_b16): within 16 lanes, lane L's
-//   element i comes from lane 4i + L/4's element L%4, so V stays row-major in
-//   LDS as loaded and P is stored [position][token] straight from the score
-//   accumulators -- no transposing stores;
-// * the next key tile's loads are issued before the current tile's compute.
+// v_mfma_f32_16x16x32_f16, for head_dim 64 and 128, in transposed form:
+// S^T = K . q^T and O^T = V^T . P^T, keys on the MFMA's M side and tokens on
+// its N side.
+// * One block per (query head, 16 TG query tokens), AC_WAVES waves; a wave
+//   takes key tiles of 32 positions round-robin with its own online softmax
+//   for all the block's tokens (TG groups of 16: one K fragment and one V^T
+//   fragment feed TG MFMAs), and the waves merge once at the end through LDS.
+// * A lane holds one token per group (r16) and eight of the tile's keys
+//   (16 t2 + 4 kg + i): a token's softmax state (m, l) is one scalar per lane;
+//   its tile maximum is a local maximum of eight and two cross-row swaps; one
+//   rescale factor covers the lane's O^T column.
+// * Scores: q (already rotated, times log2(e)/sqrt(hd), so the softmax is in
+//   base 2) enters as its f16 hi part plus the f16 rounding of the rest, so
+//   the products keep ~22 bits. K and V rows load coalesced (16-byte pieces,
+//   a 128-byte row per eight lanes) into row-major LDS tiles; the next tile's
+//   loads are issued before the current tile's softmax.
+// * P^T never goes through LDS: the score accumulators, exponentiated and
+//   split into f16 hi and lo parts, are the B operand of O^T = V^T . P^T as
+//   they stand, the MFMA's K index k = 8 kg + j standing for key 4 kg + j
+//   (j < 4) and 16 + 4 kg + j - 4 (j >= 4); the V^T operand is gathered in
+//   that key order by the gfx950 transposing LDS read (ds_read_b64_tr_b16:
+//   within 16 lanes, lane L's element i comes from lane 4i + L/4's element
+//   L%4), rows 4 kg + s/4 and 16 + 4 kg + s/4 of the row-major V tile.
+// * The reference maximum m moves only when a tile's maximum passes it by more
+//   than 8 (base 2): the exponentials stay at most 2^8, far inside f16 and
+//   f32, and O's rescale is rare instead of taken on almost every tile by
+//   some token of the wave's. Softmax is exact for any reference point; only
+//   roundings move.
 // Causality is a mask: token j keeps positions <= pos0 + j.
+//
+// A token's result does not depend on TG: its valid keys fall in the same
+// tiles, taken by the same wave in the same order (a block's extra tiles are
+// wholly masked for it: no term and no rescale), so TG is picked by the token
+// count alone (WST_ATTN_CHUNK_TG=1|2 forces one).
+//
+// Measured (0.5B shape, 14/2 heads of 64, 4096 tokens from position 0): 87 us
+// (344 TFLOP/s causal) with TG 2; TG 1 106 us. The untransposed form (scores
+// S = q . K^T, P through LDS, a row spread over 16 lanes, O's accumulators in
+// AGPRs) took 142-187 us; K operands loaded straight from the cache instead
+// of through LDS, 113-160 us.
 typedef _Float16 ac_h8 __attribute__((ext_vector_type(8)));
 typedef short ac_s4 __attribute__((ext_vector_type(4)));
-typedef short ac_s8 __attribute__((ext_vector_type(8)));
 typedef float ac_f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t ac_u4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) ac_s4 ac_lds_s4;
 
-#define AC_WAVES 8
-#define AC_TT 16  // query tokens per block
+#define AC_WAVES 4
 #define AC_KT 32  // key positions per wave iteration
 
-template <int HD>
+template <int HD, int TG>
 struct AcShape {
   static constexpr int KS = HD / 32;              // k-steps of the scores
   static constexpr int NT = HD / 16;              // 16-dim output tiles
   static constexpr int VR = HD + 16;              // V row stride (halves)
   static constexpr int KR = HD + 8;               // K row stride (halves)
-  static constexpr int PR = AC_TT;                // P row stride (halves): [pos][tok]
-  static constexpr int VU = AC_KT * HD / 8 / 64;  // 16-byte V pieces per lane per tile
-  static constexpr int WAVE_HALVES = AC_KT * VR + AC_KT * KR + 2 * AC_KT * PR;
+  static constexpr int VU = AC_KT * HD / 8 / 64;  // 16-byte K and V pieces per lane per tile
+  static constexpr int TILES = AC_KT * VR + AC_KT * KR;
+  static constexpr int MERGE = 16 * TG * (HD + 2) * 2;  // the merge rows (floats), in halves
+  static constexpr int WAVE_HALVES = TILES > MERGE ? TILES : MERGE;
   static constexpr int LDS = AC_WAVES * WAVE_HALVES * 2;
-  static_assert(16 * (HD + 2) * 4 <= WAVE_HALVES * 2, "the merge rows fit a wave's region");
 };
 
-// Eight halves as an MFMA operand from two transposing reads (rows r and r + 4
-// of the 16-lane pattern each lane's address selects).
+// Eight halves as an MFMA operand from two transposing reads (rows r and r' of
+// the 16-lane pattern each lane's address selects).
 __device__ __forceinline__ ac_h8 tr_pair(const uint16_t *a0, const uint16_t *a1) {
   const ac_s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ac_lds_s4 *)a0);
   const ac_s4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ac_lds_s4 *)a1);
   return __builtin_bit_cast(ac_h8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-template <int HD>
+__device__ __forceinline__ float row4_max(float v) {  // over the lanes r16 + 16 kg
+  RowPair p = xrow16(v);
+  v = __builtin_elementwise_maximum(p.a, p.b);
+  p = xrow32(v);
+  return __builtin_elementwise_maximum(p.a, p.b);
+}
+
+template <int HD, int TG>
 __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
     const float *__restrict__ qkv, const uint16_t *__restrict__ k_cache,
     const uint16_t *__restrict__ v_cache, uint16_t *__restrict__ out, int n_q, int n_kv,
     int pos0, int n, int max_seq, float scale) {
-  using S = AcShape<HD>;
+  using S = AcShape<HD, TG>;
+  constexpr int TT = 16 * TG;  // the block's tokens
   extern __shared__ __align__(16) uint16_t ac_lds[];
   // Token groups in reverse order: blocks are dispatched in index order, and
   // the last tokens attend to the most positions, so the longest blocks start
   // first and the short ones fill in behind them (a batched prefill's causal
   // work spans 16x between its first and last chunk).
-  const int head = blockIdx.x, t0 = (gridDim.y - 1 - blockIdx.y) * AC_TT;
+  const int head = blockIdx.x, t0 = (gridDim.y - 1 - blockIdx.y) * TT;
   const int kvh = head / (n_q / n_kv);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the tile loop is scalar
   const int r16 = lane & 15, kg = lane >> 4;
   uint16_t *vs = ac_lds + wave * S::WAVE_HALVES;  // V tile [AC_KT][VR], row-major
-  uint16_t *ph = vs + AC_KT * S::VR;              // P hi [AC_KT][PR] ([pos][tok])
-  uint16_t *pl = ph + AC_KT * S::PR;              // P lo
-  uint16_t *ks = pl + AC_KT * S::PR;              // K tile [AC_KT][KR], row-major
+  uint16_t *ks = vs + AC_KT * S::VR;              // K tile [AC_KT][KR], row-major
   const int stride_row = (n_q + 2 * n_kv) * HD;
   const uint16_t *kb = k_cache + (size_t)kvh * max_seq * HD;
   const uint16_t *vb = v_cache + (size_t)kvh * max_seq * HD;
 
-  // q of token t0 + r16 as the A operand: dims 32s + 8kg + i, hi and lo parts,
-  // scaled by log2(e) as well, so that the scores are in base 2 and the
-  // softmax exponentials are bare exp2.
+  // q^T of token t0 + 16g + r16 as the B operand: dims 32s + 8kg + i, hi and
+  // lo parts
   const float qscale = scale * 1.44269504088896340736f;
-  ac_h8 qh[S::KS], ql[S::KS];
-  {
-    const float *q = qkv + (size_t)min(t0 + r16, n - 1) * stride_row + (size_t)head * HD;
+  ac_h8 qh[TG][S::KS], ql[TG][S::KS];
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    const float *q = qkv + (size_t)min(t0 + 16 * g + r16, n - 1) * stride_row + (size_t)head * HD;
 #pragma unroll
     for (int s = 0; s < S::KS; ++s) {
       const float4 a = *(const float4 *)(q + 32 * s + 8 * kg);
@@ -213,12 +240,12 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
       for (int i = 0; i < 8; ++i) {
         const float x = v[i] * qscale;
         const _Float16 h = (_Float16)x;
-        qh[s][i] = h;
-        ql[s][i] = (_Float16)(x - (float)h);
+        qh[g][s][i] = h;
+        ql[g][s][i] = (_Float16)(x - (float)h);
       }
     }
   }
-  const int tlast = min(t0 + AC_TT, n) - 1;
+  const int tlast = min(t0 + TT, n) - 1;
   const int kend = min(pos0 + tlast + 1, max_seq);  // positions [0, kend) are attended
   const int ntiles = (kend + AC_KT - 1) / AC_KT;
 
@@ -227,8 +254,7 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   // goes in the vector offset, which is the offset the buffer range check
   // compares with num_records, so positions at or past kend read zeros
   // whatever the cache holds there (their scores are masked, their P is zero),
-  // and no load reaches past the allocation. K and V rows both load as
-  // 16-byte pieces, eight lanes to a 128-byte row, and go through LDS.
+  // and no load reaches past the allocation.
   const uint32_t kv_bytes = (uint32_t)kend * HD * 2u;
   // 0x00020000: word 3 of a raw gfx9 buffer resource (32-bit data format,
   // no swizzle); a load past kv_bytes returns zeros.
@@ -237,30 +263,31 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void *)vb, 0, (int)kv_bytes, 0x00020000);
   const uint32_t voff = (uint32_t)((lane / (HD / 8)) * HD + 8 * (lane % (HD / 8))) * 2u;
-#define AC_LOAD_TILE(KR_, VR_, KT)                                                          \
-  do {                                                                                      \
-    const uint32_t so_ = (uint32_t)(KT) * (AC_KT * HD * 2);                                \
-    _Pragma("unroll") for (int j = 0; j < S::VU; ++j) KR_[j] =                              \
-        __builtin_amdgcn_raw_buffer_load_b128(krs, so_ + voff + j * (64 / (HD / 8)) * HD * 2, \
-                                              0, 0);                                        \
-    _Pragma("unroll") for (int j = 0; j < S::VU; ++j) VR_[j] =                              \
-        __builtin_amdgcn_raw_buffer_load_b128(vrs, so_ + voff + j * (64 / (HD / 8)) * HD * 2, \
-                                              0, 0);                                        \
-  } while (0)
   ac_u4 kr[S::VU], vr[S::VU];
+  auto load_tile = [&](int kt) {
+    const uint32_t so = (uint32_t)kt * (AC_KT * HD * 2);
+#pragma unroll
+    for (int j = 0; j < S::VU; ++j)
+      kr[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, so + voff + j * (64 / (HD / 8)) * HD * 2,
+                                                    0, 0);
+#pragma unroll
+    for (int j = 0; j < S::VU; ++j)
+      vr[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, so + voff + j * (64 / (HD / 8)) * HD * 2,
+                                                    0, 0);
+  };
 
-  float m[4], l[4];
-  ac_f4 o[S::NT];
+  float m[TG], l[TG];  // per group: this lane's token; l over this lane's keys
+  ac_f4 o[TG][S::NT];  // O^T: dims 16t + 4kg + i of token 16g + r16
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    l[i] = 0.0f;
+  for (int g = 0; g < TG; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) o[g][t] = (ac_f4){0.0f, 0.0f, 0.0f, 0.0f};
   }
-#pragma unroll
-  for (int t = 0; t < S::NT; ++t) o[t] = (ac_f4){0.0f, 0.0f, 0.0f, 0.0f};
 
   int kt = wave;
-  AC_LOAD_TILE(kr, vr, min(kt, max(ntiles - 1, 0)));
+  load_tile(min(kt, max(ntiles - 1, 0)));
   while (kt < ntiles) {
     const int p0 = kt * AC_KT;
     // K and V tiles into LDS (rows past kend hold zeros; their P is zero)
@@ -270,118 +297,120 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
       *(ac_u4 *)(ks + pr * S::KR + 8 * ch) = kr[j];
       *(ac_u4 *)(vs + pr * S::VR + 8 * ch) = vr[j];
     }
-    // scores for positions p0 + 16 t2 + r16, tokens 4kg + i
-    ac_f4 sc[2];
+    // S^T for keys p0 + 16 t2 + 4kg + i, tokens 16g + r16; the A operand
+    // (key 16 t2 + r16, dims 32s + 8kg + i) read once for every group
+    ac_f4 sc[TG][2];
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      ac_f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int g = 0; g < TG; ++g) sc[g][t2] = (ac_f4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < S::KS; ++s) {
-        const ac_h8 b = *(const ac_h8 *)(ks + (16 * t2 + r16) * S::KR + 32 * s + 8 * kg);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], b, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[s], b, c, 0, 0, 0);
+        const ac_h8 a = *(const ac_h8 *)(ks + (16 * t2 + r16) * S::KR + 32 * s + 8 * kg);
+#pragma unroll
+        for (int g = 0; g < TG; ++g) {
+          sc[g][t2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[g][s], sc[g][t2], 0, 0, 0);
+          sc[g][t2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[g][s], sc[g][t2], 0, 0, 0);
+        }
       }
-      sc[t2] = c;
     }
     // the next tile's loads go out now (the registers above are consumed)
-    const int next = kt + AC_WAVES;
-    AC_LOAD_TILE(kr, vr, min(next, ntiles - 1));
-    // online softmax per token row (register i), the row spread over 16 lanes.
+    load_tile(min(kt + AC_WAVES, ntiles - 1));
     // A tile wholly below the block's first token's limit and the cache end
-    // (most of them) needs no mask: the same values without the selects.
-    float corr[4];
+    // (most of them) needs no mask.
     const bool full = p0 + AC_KT - 1 <= pos0 + t0 && p0 + AC_KT <= kend;  // uniform
-    if (full) {
+    float corr[TG];
+    ac_h8 pbh[TG], pbl[TG];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float mx = dpp_max16(__builtin_elementwise_maximum(sc[0][i], sc[1][i]));
-        const float mn = __builtin_elementwise_maximum(m[i], mx);
-        corr[i] = (m[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[i] - mn);
-        const float pv0 = __builtin_amdgcn_exp2f(sc[0][i] - mn);
-        const float pv1 = __builtin_amdgcn_exp2f(sc[1][i] - mn);
-        l[i] = l[i] * corr[i] + pv0 + pv1;  // this lane's columns; rows reduce at the end
-        m[i] = mn;
-        sc[0][i] = pv0;
-        sc[1][i] = pv1;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int lim = pos0 + t0 + 4 * kg + i;  // last position this token attends
-        float sv[2];
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          const int p = p0 + 16 * t2 + r16;
-          sv[t2] = (p <= lim && p < kend) ? sc[t2][i] : -INFINITY;
-        }
-        const float mx = dpp_max16(__builtin_elementwise_maximum(sv[0], sv[1]));
-        const float mn = __builtin_elementwise_maximum(m[i], mx);
-        corr[i] = (m[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[i] - mn);
-        float pv[2];
+    for (int g = 0; g < TG; ++g) {
+      if (!full) {
+        const int lim = pos0 + t0 + 16 * g + r16;  // the last position this token attends
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2)
-          pv[t2] = (sv[t2] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sv[t2] - mn);
-        l[i] = l[i] * corr[i] + pv[0] + pv[1];
-        m[i] = mn;
-        sc[0][i] = pv[0];
-        sc[1][i] = pv[1];
-      }
-    }
-    // P (hi, lo) to LDS as [pos][tok]: one 8-byte store per tile and part
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      uint16_t hv[4], lv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const _Float16 h = (_Float16)sc[t2][i];
-        hv[i] = __builtin_bit_cast(uint16_t, h);
-        lv[i] = __builtin_bit_cast(uint16_t, (_Float16)(sc[t2][i] - (float)h));
+          for (int i = 0; i < 4; ++i) {
+            const int p = p0 + 16 * t2 + 4 * kg + i;
+            if (!(p <= lim && p < kend)) sc[g][t2][i] = -INFINITY;
+          }
       }
-      const int row = 16 * t2 + r16;
-      *(uint2 *)(ph + row * S::PR + 4 * kg) =
-          make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
-      *(uint2 *)(pl + row * S::PR + 4 * kg) =
-          make_uint2(lv[0] | ((uint32_t)lv[1] << 16), lv[2] | ((uint32_t)lv[3] << 16));
+#define AC_MAX(a, b) __builtin_elementwise_maximum(a, b)
+      float mx = AC_MAX(AC_MAX(AC_MAX(sc[g][0][0], sc[g][0][1]), AC_MAX(sc[g][0][2], sc[g][0][3])),
+                        AC_MAX(AC_MAX(sc[g][1][0], sc[g][1][1]), AC_MAX(sc[g][1][2], sc[g][1][3])));
+#undef AC_MAX
+      mx = row4_max(mx);
+      // m moves only past m + 8; mx = -inf (no key of this token in the
+      // tile) leaves it
+      const bool bump = mx > m[g] + 8.0f;
+      const float mn = bump ? mx : m[g];
+      corr[g] = !bump ? 1.0f : (m[g] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[g] - mn);
+      // exp2(-inf - mref) = 0 for a masked score; mref is finite so that a
+      // token with no key yet (mn = -inf) gets 0, not NaN
+      const float mref = (mn == -INFINITY) ? 0.0f : mn;
+      float pv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(sc[g][j >> 2][j & 3] - mref);
+      // P^T hi and lo as B operands (k = 8kg + j <-> key, above); the hi
+      // parts converted in pairs
+      float psum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        psum += pv[j];
+        psum += pv[j + 1];
+        const auto h2 = __builtin_amdgcn_cvt_pkrtz(pv[j], pv[j + 1]);
+        pbh[g][j] = h2[0];
+        pbh[g][j + 1] = h2[1];
+        pbl[g][j] = (_Float16)(pv[j] - (float)h2[0]);
+        pbl[g][j + 1] = (_Float16)(pv[j + 1] - (float)h2[1]);
+      }
+      l[g] = l[g] * corr[g] + psum;
+      m[g] = mn;
     }
-    // O's rescale, skipped when no row's maximum moved in the whole wave
-    // (every factor 1: the products would be exact copies).
-    const bool same = corr[0] == 1.0f && corr[1] == 1.0f && corr[2] == 1.0f && corr[3] == 1.0f;
-    if (!__all(same)) {  // some lane of the wave has a factor != 1
+    // O's rescale, skipped when no token's factor in the wave moved (every
+    // factor 1: the products would be exact copies)
+    bool same = true;
+#pragma unroll
+    for (int g = 0; g < TG; ++g) same = same && corr[g] == 1.0f;
+    if (!__all(same)) {
+#pragma unroll
+      for (int g = 0; g < TG; ++g)
 #pragma clang loop unroll(full)
-      for (int t = 0; t < S::NT; ++t)
+        for (int t = 0; t < S::NT; ++t)
 #pragma clang loop unroll(full)
-        for (int i = 0; i < 4; ++i) o[t][i] *= corr[i];
+          for (int i = 0; i < 4; ++i) o[g][t][i] *= corr[g];
     }
-    // A operand: P[tok = r16][pos = 8kg + i]; source lane s reads row 8kg + s/4 (+4), cols 4(s%4)
-    const int sr = 8 * kg + (r16 >> 2), sc4 = 4 * (r16 & 3);
-    const ac_h8 pah = tr_pair(ph + sr * S::PR + sc4, ph + (sr + 4) * S::PR + sc4);
-    const ac_h8 pal = tr_pair(pl + sr * S::PR + sc4, pl + (sr + 4) * S::PR + sc4);
+    // V^T operand: lane s of a 16-lane group reads key rows 4kg + s/4 and
+    // 16 + 4kg + s/4, dims 16t + 4(s%4); one read serves every group
+    const int sr = 4 * kg + (r16 >> 2), sc4 = 4 * (r16 & 3);
 #pragma clang loop unroll(full)
     for (int t = 0; t < S::NT; ++t) {
-      // B operand: V[pos = 8kg + i][dim = 16t + r16]
-      const ac_h8 bv = tr_pair(vs + sr * S::VR + 16 * t + sc4, vs + (sr + 4) * S::VR + 16 * t + sc4);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, bv, o[t], 0, 0, 0);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pal, bv, o[t], 0, 0, 0);
-    }
-    kt = next;
-  }
-#undef AC_LOAD_TILE
-
-  // merge the waves: rows 4kg + i, per wave (m, l, O[row][HD])
-  float *mb = (float *)vs;  // this wave's region, [16][HD + 2]
+      const ac_h8 va =
+          tr_pair(vs + sr * S::VR + 16 * t + sc4, vs + (sr + 16) * S::VR + 16 * t + sc4);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float lr = dpp_sum16(l[i]);
-    const int row = 4 * kg + i;
-    if (r16 == 0) {
-      mb[row * (HD + 2)] = m[i];
+      for (int g = 0; g < TG; ++g) {
+        o[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbh[g], o[g][t], 0, 0, 0);
+        o[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbl[g], o[g][t], 0, 0, 0);
+      }
+    }
+    kt += AC_WAVES;
+  }
+
+  // merge the waves: per wave (m, l, O[tok][HD]), rows 16g + r16
+  float *mb = (float *)vs;  // this wave's region, [TT][HD + 2]
+#pragma unroll
+  for (int g = 0; g < TG; ++g) {
+    const int row = 16 * g + r16;
+    const float lr = row4_sum(l[g]);
+    if (kg == 0) {
+      mb[row * (HD + 2)] = m[g];
       mb[row * (HD + 2) + 1] = lr;
     }
 #pragma unroll
-    for (int t = 0; t < S::NT; ++t) mb[row * (HD + 2) + 2 + 16 * t + r16] = o[t][i];
+    for (int t = 0; t < S::NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mb[row * (HD + 2) + 2 + 16 * t + 4 * kg + i] = o[g][t][i];
   }
   __syncthreads();
-  const int rows = min(AC_TT, n - t0);
+  const int rows = min(TT, n - t0);
   for (int idx = tid; idx < rows * HD; idx += AC_WAVES * 64) {
     const int row = idx / HD, d = idx % HD;
     float M = -INFINITY;
@@ -400,19 +429,34 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   }
 }
 
+template <int HD, int TG>
+static void attn_chunk_mfma_tg(const void *qkv, const void *k_cache, const void *v_cache,
+                               void *out, int n_q, int n_kv, int pos0, int n, int max_seq,
+                               float scale) {
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void *)attn_chunk_mfma_kernel<HD, TG>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, AcShape<HD, TG>::LDS);
+    attr = true;
+  }
+  const dim3 grid(n_q, (n + 16 * TG - 1) / (16 * TG));
+  attn_chunk_mfma_kernel<HD, TG><<<grid, AC_WAVES * 64, AcShape<HD, TG>::LDS, WST_STREAM>>>(
+      (const float *)qkv, (const uint16_t *)k_cache, (const uint16_t *)v_cache, (uint16_t *)out,
+      n_q, n_kv, pos0, n, max_seq, scale);
+}
+
+// Two groups of 16 tokens per wave from 512 tokens up (0.5B shape, 4096
+// tokens: 87 against 106 us); one below (7B shape, 256 tokens: 10.0 against
+// 11.7 us, the blocks twice as many).
 template <int HD>
 static void attn_chunk_mfma(const void *qkv, const void *k_cache, const void *v_cache, void *out,
                             int n_q, int n_kv, int pos0, int n, int max_seq, float scale) {
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void *)attn_chunk_mfma_kernel<HD>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, AcShape<HD>::LDS);
-    attr = true;
-  }
-  const dim3 grid(n_q, (n + AC_TT - 1) / AC_TT);
-  attn_chunk_mfma_kernel<HD><<<grid, AC_WAVES * 64, AcShape<HD>::LDS, WST_STREAM>>>(
-      (const float *)qkv, (const uint16_t *)k_cache, (const uint16_t *)v_cache, (uint16_t *)out,
-      n_q, n_kv, pos0, n, max_seq, scale);
+  const char *v = getenv("WST_ATTN_CHUNK_TG");
+  const int tg = (v && (v[0] == '1' || v[0] == '2')) ? v[0] - '0' : (n >= 512 ? 2 : 1);
+  if (tg == 2)
+    attn_chunk_mfma_tg<HD, 2>(qkv, k_cache, v_cache, out, n_q, n_kv, pos0, n, max_seq, scale);
+  else
+    attn_chunk_mfma_tg<HD, 1>(qkv, k_cache, v_cache, out, n_q, n_kv, pos0, n, max_seq, scale);
 }
 
 extern "C" wst_status_t wst_attn_chunk(const void *qkv, const void *k_cache, const void *v_cache,

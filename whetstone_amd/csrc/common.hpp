@@ -176,6 +176,9 @@ __device__ __forceinline__ float xrow32_sum(float v) {
   const RowPair p = xrow32(v);
   return p.a + p.b;
 }
+// Sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48); every
+// lane gets the same bits (each step adds a pair, which commutes).
+__device__ __forceinline__ float row4_sum(float v) { return xrow32_sum(xrow16_sum(v)); }
 
 // Sum over the 32 lanes of each half wave, returned in every lane of that half.
 __device__ __forceinline__ float half_wave_sum(float v) { return xrow16_sum(dpp_sum16(v)); }
@@ -302,6 +305,19 @@ __device__ __forceinline__ void qk_norm(float &x1, float &x2, const uint16_t *__
                                         float *red) {
   const float a = active ? fmaf(x1, x1, x2 * x2) : 0.0f;
   const float ss = block_sum(a, red);
+  const float s = 1.0f / sqrtf(ss / (float)hd + eps);
+  if (active) {
+    x1 = x1 * s * h2f(g[j]);
+    x2 = x2 * s * h2f(g[j + half]);
+  }
+}
+
+// qk_norm for a head held by one wave (not a whole block): the same sum, as
+// block_sum over a one-wave block returns the wave's sum.
+__device__ __forceinline__ void qk_norm_wave(float &x1, float &x2,
+                                             const uint16_t *__restrict__ g, int j, int half,
+                                             int hd, float eps, bool active) {
+  const float ss = wave_sum(active ? fmaf(x1, x1, x2 * x2) : 0.0f);
   const float s = 1.0f / sqrtf(ss / (float)hd + eps);
   if (active) {
     x1 = x1 * s * h2f(g[j]);

@@ -695,100 +695,206 @@ __global__ __launch_bounds__(512) void gemm_reduce_norm_kernel(
     h[base + c] = f2h(xrow[c] * sc * h2f(nw[c]));
 }
 
-// Fused reduce + QK-norm + RoPE + KV append, one 64-thread block per (head,
-// token) as rope_cache_kernel (head_dim <= 128, so a head's halves are one
-// wave): the head's qkv values are summed from the splits (+ bias) exactly as
-// gemm_split_reduce_kernel does and stored to qkv, then rotated exactly as
-// rope_cache_kernel does (q back into qkv, k and v to the cache).
-__global__ __launch_bounds__(64) void gemm_reduce_rope_kernel(
+// gemm_reduce_norm_kernel for rows of out_f <= 4096 columns, out_f % 8 == 0:
+// a token per block of 64 * ceil(out_f / 512) threads, thread t holding the
+// eight columns 8t..8t+7 (two 16-byte loads per operand). rms_scale512 gives
+// thread t of its 512 exactly these eight columns, in this order, for rows of
+// at most 4096 columns, and its threads past the row add zeros, as the missing
+// waves here do: both outputs are bit-identical to the 512-thread form. (The
+// 512-thread form with two columns a thread ran 16 us over 4096 tokens of 896
+// columns: 4096 barrier-bound blocks.)
+__global__ __launch_bounds__(512) void gemm_reduce_norm8_kernel(
+    const float *__restrict__ ws, const uint16_t *__restrict__ bias, float *__restrict__ y,
+    int out_f, int n, int splits, int accum, const uint16_t *__restrict__ nw, float eps,
+    uint16_t *__restrict__ h) {
+  __shared__ float red[16];
+  const int tok = blockIdx.x;
+  const size_t total = (size_t)n * out_f, base = (size_t)tok * out_f;
+  const int c0 = 8 * (int)threadIdx.x;
+  const bool on = c0 < out_f;
+  float t[8];
+  float acc = 0.0f;
+  if (on) {
+    float v[8];
+    const float4 *w0 = (const float4 *)(ws + base + c0);
+    float4 a = w0[0], b = w0[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    for (int z = 1; z < splits; ++z) {  // split order, as split_sum
+      const float4 *wz = (const float4 *)(ws + (size_t)z * total + base + c0);
+      a = wz[0];
+      b = wz[1];
+      v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+      v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+    }
+    if (bias) {
+      const uint4 bb = *(const uint4 *)(bias + c0);
+      const uint32_t bw[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] += h2f((uint16_t)(bw[e] & 0xFFFFu));
+        v[2 * e + 1] += h2f((uint16_t)(bw[e] >> 16));
+      }
+    }
+    if (accum) {
+      const float4 *yr = (const float4 *)(y + base + c0);
+      a = yr[0];
+      b = yr[1];
+      const float yv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = yv[e] + v[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = v[e];
+    }
+    float4 *yo = (float4 *)(y + base + c0);
+    yo[0] = make_float4(t[0], t[1], t[2], t[3]);
+    yo[1] = make_float4(t[4], t[5], t[6], t[7]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(t[e], t[e], acc);
+  }
+  acc = block_sum(acc, red);
+  const float sc = 1.0f / sqrtf(acc / (float)out_f + eps);
+  if (!on) return;
+  const uint4 gw = *(const uint4 *)(nw + c0);
+  const uint32_t g[4] = {gw.x, gw.y, gw.z, gw.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint16_t lo = f2h(t[2 * e] * sc * h2f((uint16_t)(g[e] & 0xFFFFu)));
+    const uint16_t hi = f2h(t[2 * e + 1] * sc * h2f((uint16_t)(g[e] >> 16)));
+    o[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+  }
+  *(uint4 *)(h + base + c0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Fused reduce + QK-norm + RoPE + KV append (head_dim <= 128, so a head's
+// halves are one wave): the head's qkv values are summed from the splits
+// (+ bias) exactly as gemm_split_reduce_kernel does and stored to qkv, then
+// rotated exactly as rope_cache_kernel does (q back into qkv, k and v to the
+// cache). The QK-norm sum is the wave's sum, which is what a one-wave block's
+// block_sum returns (its second stage adds the one wave total to 0).
+//
+// A wave per (token, head) item, four waves a block (as fast as a 64-thread
+// block per item: 25 us over 4096 tokens x 18 heads, 38 MB; a wave taking
+// eight items, their loads all issued before the first rotation or only the
+// next item's ahead, 32-33 us).
+#define RR_WAVES 4
+#define RR_ITEMS 1
+struct RrIn {
+  float v[4];  // the item's reduced columns held by this lane
+  float c, s;  // its rotation factors
+};
+__global__ __launch_bounds__(64 * RR_WAVES) void gemm_reduce_rope_kernel(
     const float *__restrict__ ws, const uint16_t *__restrict__ bias, float *__restrict__ qkv,
     int splits, int n, uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache,
     const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, int n_q, int n_kv,
     int hd, int pos0, int max_seq, const uint16_t *__restrict__ q_norm_w,
     const uint16_t *__restrict__ k_norm_w, float eps) {
-  __shared__ float red[16];
-  const int head = blockIdx.x, tok = blockIdx.y;
-  const int half = hd >> 1, j = threadIdx.x;
-  const bool active = j < half;
+  const int nh = n_q + n_kv, items = n * nh;
+  const int first = (blockIdx.x * RR_WAVES + (int)(threadIdx.x >> 6)) * RR_ITEMS;
+  if (first >= items) return;  // a whole wave: no barriers below
+  const int last = min(first + RR_ITEMS, items);
+  const int half = hd >> 1, j = threadIdx.x & 63;
   const int nqkv = (n_q + 2 * n_kv) * hd;
   const size_t total = (size_t)n * nqkv;
-  float *row = qkv + (size_t)tok * nqkv;
-  const float *wrow = ws + (size_t)tok * nqkv;
-  auto red_at = [&](int c) {  // the split sum of column c (stored to qkv)
-    float t = split_sum(wrow, c, total, splits);
-    if (bias) t += h2f(bias[c]);
-    row[c] = t;
-    return t;
+  // Lane roles. half <= 32: one column per lane (lanes 0..31 the first half,
+  // 32..63 the second), the rotation partner over a cross-lane swap; else
+  // lane j < half holds columns j and j + half. The norm's sum and every
+  // product are the same in both forms.
+  const bool narrow = half <= 32;
+  const bool hi = narrow && j >= 32;
+  const int jj = narrow ? (j & 31) : j;
+  const bool act = jj < half;
+  const int off = jj + (hi ? half : 0);
+  // column e of item (head) relative to the row: q heads use e = 0 (and 1
+  // in the wide form), kv heads k then v
+  auto col = [&](int head, int e) {
+    if (head < n_q) return head * hd + (narrow ? off : jj + e * half);
+    const int kvh = head - n_q;
+    const int k0 = (n_q + kvh) * hd, v0 = (n_q + n_kv + kvh) * hd;
+    if (narrow) return (e == 0 ? k0 : v0) + off;
+    return (e < 2 ? k0 : v0) + jj + (e & 1) * half;
   };
-  const int pos = min(max(pos0 + tok, 0), max_seq - 1);
-  if (half <= 32) {
-    // One column per lane (lanes 0..31: the first half, 32..63: the second),
-    // the rotation partner over a cross-lane swap; the norm's sum and every
-    // product are those of the two-columns-per-lane form below.
-    const bool hi = j >= 32;
-    const int jj = j & 31;
-    const bool act = jj < half;
-    const int off = jj + (hi ? half : 0);
-    const float c = act ? cos_tab[(size_t)pos * half + jj] : 0.0f;
-    const float s = act ? sin_tab[(size_t)pos * half + jj] : 0.0f;
-    auto rotate = [&](float mine, const uint16_t *__restrict__ g, float &lo, float &hv) {
+  auto ncols = [&](int head) { return (head < n_q ? 1 : 2) * (narrow ? 1 : 2); };
+  auto fetch = [&](int it, RrIn &r) {
+    const int head = it % nh, tok = it / nh;
+    const float *wrow = ws + (size_t)tok * nqkv;
+    const int pos = min(max(pos0 + tok, 0), max_seq - 1);
+    const int nc = ncols(head);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float t = 0.0f;
+      if (act && e < nc) {
+        const int c = col(head, e);
+        t = split_sum(wrow, c, total, splits);
+        if (bias) t += h2f(bias[c]);
+      }
+      r.v[e] = t;
+    }
+    r.c = act ? cos_tab[(size_t)pos * half + jj] : 0.0f;
+    r.s = act ? sin_tab[(size_t)pos * half + jj] : 0.0f;
+  };
+  RrIn in[RR_ITEMS];
+#pragma unroll
+  for (int k = 0; k < RR_ITEMS; ++k)
+    if (first + k < last) fetch(first + k, in[k]);
+#pragma unroll
+  for (int k = 0; k < RR_ITEMS; ++k) {
+    const int it = first + k;
+    if (it >= last) break;
+    const RrIn &cur = in[k];
+    const int head = it % nh, tok = it / nh;
+    float *row = qkv + (size_t)tok * nqkv;
+    const int pos = min(max(pos0 + tok, 0), max_seq - 1);
+    const int nc = ncols(head);
+    if (act) {  // the reduced values, as gemm_split_reduce_kernel stores them
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < nc) row[col(head, e)] = cur.v[e];
+    }
+    const float c = cur.c, s = cur.s;
+    const bool is_q = head < n_q;
+    const uint16_t *__restrict__ g = is_q ? q_norm_w : k_norm_w;
+    if (narrow) {
+      const float mine = cur.v[0];
       const float other = __shfl_xor(mine, 32);
       float x1 = hi ? other : mine, x2 = hi ? mine : other;
       if (g) {
-        const float ss = block_sum(act && !hi ? fmaf(x1, x1, x2 * x2) : 0.0f, red);
+        const float ss = wave_sum(act && !hi ? fmaf(x1, x1, x2 * x2) : 0.0f);
         const float sc = 1.0f / sqrtf(ss / (float)hd + eps);
         if (act) {
           x1 = x1 * sc * h2f(g[jj]);
           x2 = x2 * sc * h2f(g[jj + half]);
         }
       }
-      lo = rope_lo(x1, x2, c, s);
-      hv = rope_hi(x1, x2, c, s);
-    };
-    float lo, hv;
-    if (head < n_q) {
-      const int q0 = head * hd;
-      const float mine = act ? red_at(q0 + off) : 0.0f;
-      rotate(mine, q_norm_w, lo, hv);
-      if (act) row[q0 + off] = hi ? hv : lo;
-      return;
+      const float lo = rope_lo(x1, x2, c, s), hv = rope_hi(x1, x2, c, s);
+      if (act) {
+        if (is_q) {
+          row[col(head, 0)] = hi ? hv : lo;
+        } else {
+          const size_t slot = ((size_t)(head - n_q) * max_seq + pos) * hd;
+          k_cache[slot + off] = f2h(hi ? hv : lo);
+          v_cache[slot + off] = f2h(cur.v[1]);
+        }
+      }
+    } else {
+      float x1 = cur.v[0], x2 = cur.v[1];
+      if (g) qk_norm_wave(x1, x2, g, jj, half, hd, eps, act);
+      if (act) {
+        if (is_q) {
+          row[head * hd + jj] = rope_lo(x1, x2, c, s);
+          row[head * hd + jj + half] = rope_hi(x1, x2, c, s);
+        } else {
+          const size_t slot = ((size_t)(head - n_q) * max_seq + pos) * hd;
+          k_cache[slot + jj] = f2h(rope_lo(x1, x2, c, s));
+          k_cache[slot + jj + half] = f2h(rope_hi(x1, x2, c, s));
+          v_cache[slot + jj] = f2h(cur.v[2]);
+          v_cache[slot + jj + half] = f2h(cur.v[3]);
+        }
+      }
     }
-    const int kvh = head - n_q;
-    const int k0 = (n_q + kvh) * hd, v0 = (n_q + n_kv + kvh) * hd;
-    const float km = act ? red_at(k0 + off) : 0.0f;
-    const float vm = act ? red_at(v0 + off) : 0.0f;
-    rotate(km, k_norm_w, lo, hv);
-    if (!act) return;
-    const size_t slot = ((size_t)kvh * max_seq + pos) * hd;
-    k_cache[slot + off] = f2h(hi ? hv : lo);
-    v_cache[slot + off] = f2h(vm);
-    return;
   }
-  const float c = active ? cos_tab[(size_t)pos * half + j] : 0.0f;
-  const float s = active ? sin_tab[(size_t)pos * half + j] : 0.0f;
-  if (head < n_q) {
-    const int q0 = head * hd;
-    float x1 = active ? red_at(q0 + j) : 0.0f;
-    float x2 = active ? red_at(q0 + j + half) : 0.0f;
-    if (q_norm_w) qk_norm(x1, x2, q_norm_w, j, half, hd, eps, active, red);
-    if (!active) return;
-    row[q0 + j] = rope_lo(x1, x2, c, s);
-    row[q0 + j + half] = rope_hi(x1, x2, c, s);
-    return;
-  }
-  const int kvh = head - n_q;
-  const int k0 = (n_q + kvh) * hd, v0 = (n_q + n_kv + kvh) * hd;
-  float k1 = active ? red_at(k0 + j) : 0.0f;
-  float k2 = active ? red_at(k0 + j + half) : 0.0f;
-  const float va = active ? red_at(v0 + j) : 0.0f;
-  const float vb = active ? red_at(v0 + j + half) : 0.0f;
-  if (k_norm_w) qk_norm(k1, k2, k_norm_w, j, half, hd, eps, active, red);
-  if (!active) return;
-  const size_t slot = ((size_t)kvh * max_seq + pos) * hd;
-  k_cache[slot + j] = f2h(rope_lo(k1, k2, c, s));
-  k_cache[slot + j + half] = f2h(rope_hi(k1, k2, c, s));
-  v_cache[slot + j] = f2h(va);
-  v_cache[slot + j + half] = f2h(vb);
 }
 
 namespace {
@@ -1031,6 +1137,15 @@ extern "C" wst_status_t wst_gemm_hier_norm_chunks(const void *qw, const void *si
                               hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4);
     attr = true;
   }
+  if (out_f % 8 == 0 && out_f <= 4096 && !(((uintptr_t)y | (uintptr_t)h_out | (uintptr_t)norm_w |
+                                              (uintptr_t)bias) & 15u)) {
+    const int threads = 64 * ((out_f / 8 + 63) / 64);
+    gemm_reduce_norm8_kernel<<<n, threads, 0, WST_STREAM>>>(
+        ws, (const uint16_t *)bias, (float *)y, out_f, n, splits, accum, (const uint16_t *)norm_w,
+        eps, (uint16_t *)h_out);
+    WST_TRY_KERNEL("wst_gemm_hier_norm_chunk");
+    return WST_OK;
+  }
   auto kern = out_f <= 1024   ? gemm_reduce_norm_kernel<2>
               : out_f <= 2048 ? gemm_reduce_norm_kernel<4>
               : out_f <= 4096 ? gemm_reduce_norm_kernel<8>
@@ -1073,7 +1188,8 @@ extern "C" wst_status_t wst_gemm_hier_rope_chunks(const void *qw, const void *si
   int splits;
   st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits, plan_n);
   if (st != WST_OK) return st;
-  gemm_reduce_rope_kernel<<<dim3(n_q + n_kv, n), 64, 0, WST_STREAM>>>(
+  const int rr_waves = ((n_q + n_kv) * n + RR_ITEMS - 1) / RR_ITEMS;
+  gemm_reduce_rope_kernel<<<(rr_waves + RR_WAVES - 1) / RR_WAVES, 64 * RR_WAVES, 0, WST_STREAM>>>(
       ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,
       (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv, head_dim,
       pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
