@@ -357,6 +357,33 @@ def test_argmax_equals_oracle_key_argmax(orc, wk, n):
         assert idx.numpy()[0] == orc.argmax(v)
 
 
+@pytest.mark.parametrize("vocab,n", [(151936, 5), (152064, 3), (1001, 4), (8, 2), (40000, 1)])
+def test_argmax_rows_equals_oracle_key_argmax(orc, wk, vocab, n):
+    """wst_argmax_chunk, a row per token (chunk_ops.cu:425-468): every row's
+    pick equals the oracle's key argmax (ties to the lowest index, the
+    special values ordered as the single-row argmax orders them). Vocab sizes
+    that are a multiple of 4 take the 16-byte-load form, 1001 the scalar one;
+    the last row starts 4 bytes off a 16-byte boundary when vocab is odd."""
+    rng = np.random.default_rng(vocab + n)
+    v = rng.standard_normal(n * vocab).astype(np.float32).reshape(n, vocab)
+    if vocab > 10:
+        for r in range(n):
+            v[r, rng.integers(0, vocab, 3)] = v[r].max()  # planted ties
+        v[0, 5] = np.inf
+        v[0, 6] = -np.inf
+        v[n - 1, vocab - 1] = v[n - 1].max() + 1.0  # the pick in the last 16-byte piece
+        if n > 1:
+            v[1, :] = -0.0
+            v[1, vocab // 2] = 0.0
+    d = wk.DeviceBuffer.from_array(v.reshape(-1))
+    out = wk.DeviceBuffer(n, np.int32)
+    print(f"argmax rows: vocab {vocab} n {n}", flush=True)
+    ffi.call("wst_argmax_chunk", d.ptr, out.ptr, vocab, n)
+    got = out.numpy()
+    for r in range(n):
+        assert got[r] == orc.argmax(v[r]), r
+
+
 def test_nll_matches_host_log_softmax(wk):
     """decode_kernels.rs:434-460."""
     n = 151936

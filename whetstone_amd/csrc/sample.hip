@@ -117,10 +117,54 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float *__restric
   }
 }
 
+// The same for rows of a multiple of 4 logits on 16-byte boundaries: 1024
+// threads a row, 16-byte loads, four in flight per thread (the key maximum
+// does not depend on the order: same result). The 256-thread form with one
+// 4-byte load per iteration waited out a load per step: 204 us over 256
+// rows of 151936 logits (155 MB).
+__global__ __launch_bounds__(1024) void argmax_rows4_kernel(const float *__restrict__ logits,
+                                                           int vocab, int32_t *__restrict__ out) {
+  __shared__ unsigned long long wbest[16];
+  const float4 *row = (const float4 *)(logits + (size_t)blockIdx.x * vocab);
+  const int n4 = vocab >> 2;
+  unsigned long long best = 0ull;
+  int i = threadIdx.x;
+  for (; i + 3 * 1024 < n4; i += 4 * 1024) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = row[i + u * 1024];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int b = 4 * (i + u * 1024);
+      best = u64_max(best, u64_max(u64_max(argmax_key(v[u].x, b), argmax_key(v[u].y, b + 1)),
+                                   u64_max(argmax_key(v[u].z, b + 2), argmax_key(v[u].w, b + 3))));
+    }
+  }
+  for (; i < n4; i += 1024) {
+    const float4 v = row[i];
+    const int b = 4 * i;
+    best = u64_max(best, u64_max(u64_max(argmax_key(v.x, b), argmax_key(v.y, b + 1)),
+                                 u64_max(argmax_key(v.z, b + 2), argmax_key(v.w, b + 3))));
+  }
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = wbest[0];
+    for (int w = 1; w < 16; ++w) b = u64_max(b, wbest[w]);
+    out[blockIdx.x] = (int32_t)(~(uint32_t)(b & 0xFFFFFFFFull));
+  }
+}
+
 extern "C" wst_status_t wst_argmax_chunk(const void *logits, void *out, int32_t vocab,
                                          int32_t n) {
   WST_REQUIRE(logits && out, "wst_argmax_chunk: null pointer");
   WST_REQUIRE(vocab > 0 && n > 0, "wst_argmax_chunk: bad shape");
+  if (vocab % 4 == 0 && !((uintptr_t)logits & 15u)) {
+    argmax_rows4_kernel<<<n, 1024, 0, WST_STREAM>>>((const float *)logits, vocab, (int32_t *)out);
+    WST_TRY_KERNEL("wst_argmax_chunk");
+    return WST_OK;
+  }
   argmax_rows_kernel<<<n, 256, 0, WST_STREAM>>>((const float *)logits, vocab, (int32_t *)out);
   WST_TRY_KERNEL("wst_argmax_chunk");
   return WST_OK;
