@@ -610,6 +610,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
 #define GM_MAXSPLIT 16
 __device__ __forceinline__ float split_sum(const float *__restrict__ ws, size_t i, size_t total,
                                            int splits) {
+  if (splits == 1) return ws[i];  // (the batch of four below would load it four times)
   float t = 0.0f;
   for (int z0 = 0; z0 < splits; z0 += 4) {
     float v[4];
@@ -848,7 +849,8 @@ __global__ __launch_bounds__(64 * RR_WAVES) void gemm_reduce_rope_kernel(
     float *row = qkv + (size_t)tok * nqkv;
     const int pos = min(max(pos0 + tok, 0), max_seq - 1);
     const int nc = ncols(head);
-    if (act) {  // the reduced values, as gemm_split_reduce_kernel stores them
+    if (act && head >= n_q) {  // k and v: the reduced values, as gemm_split_reduce_kernel
+                               // stores them (q's are overwritten below by their rotation)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (e < nc) row[col(head, e)] = cur.v[e];
