@@ -11,8 +11,9 @@ References:
     computed here (first-step logits, and the same step under the oracle's
     two f32 summation orders);
   * tests/golden/qwen7b_ctx2048_greedy.json, written by the oracle in the
-    build container: 64 greedy tokens with their top-2 margins and a sample
-    of the first step's logits; and under "ref" the same step and stream in
+    build container: 256 greedy tokens (context 2048 -> 2304) with their
+    top-2 margins and a sample of the first step's logits; and under "ref"
+    the same step and stream in
     the oracle's ORC_ACC_REF mode, which restates the reference CUDA build's
     own arithmetic (f16 __hfma2/__hadd2 group sums in the GEMV,
     gemv_hier.cu:118-163; its reduction orders; its attention splits on a
