@@ -514,7 +514,6 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
 #define GW_STEP(U)                                                              \
   {                                                                             \
     const int st = st0 + (U);                                                   \
-    if (st >= steps) break;                                                     \
     issue_x(st + GW_DX - 1);                                                    \
     issue_w(st + GW_DW, wq[(U) % GW_DW], wi[(U) % GW_DW]);                      \
     GW_WAIT(((U) + 1) % GW_DW, S::VMCNT)                                        \
@@ -522,17 +521,40 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
     store_w(wq[((U) + 1) % GW_DW], wi[((U) + 1) % GW_DW], st + 1, (st + 1) & 1); \
     __syncthreads();                                                            \
   }
-  for (int st0 = 0; st0 < steps; st0 += GW_DW) {
+  // Whole rounds of GW_DW steps in a loop with no exit inside it, then the
+  // remaining steps. (With a `break` after each step inside one loop, the
+  // compiler rotated the accumulators through other registers every step:
+  // 16 v_mov_b64 behind an MFMA drain.)
+  int st0 = 0;
+  for (; st0 + GW_DW <= steps; st0 += GW_DW) {
     GW_STEP(0)
     GW_STEP(1)
     GW_STEP(2)
     GW_STEP(3)
   }
+  if (st0 < steps) GW_STEP(0)
+  if (st0 + 1 < steps) GW_STEP(1)
+  if (st0 + 2 < steps) GW_STEP(2)
 #undef GW_STEP
 #undef GW_WAIT
   // Clamped look-ahead DMAs may still be landing in the ring, which the
-  // epilogue tile overlaps.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // epilogue tile overlaps; and the look-ahead weight loads of the last
+  // steps may still be landing in their ring registers. Those registers are
+  // operands of this wait, so the compiler keeps them reserved until it (a
+  // dead load destination it took back earlier would be overwritten when the
+  // load lands).
+  if constexpr (RPT == 1)
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(wq[0][0]), "+v"(wi[0][0]), "+v"(wq[1][0]), "+v"(wi[1][0]),
+                   "+v"(wq[2][0]), "+v"(wi[2][0]), "+v"(wq[3][0]), "+v"(wi[3][0])
+                 :: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(wq[0][0]), "+v"(wi[0][0]), "+v"(wq[1][0]), "+v"(wi[1][0]),
+                   "+v"(wq[2][0]), "+v"(wi[2][0]), "+v"(wq[3][0]), "+v"(wi[3][0]),
+                   "+v"(wq[0][1]), "+v"(wi[0][1]), "+v"(wq[1][1]), "+v"(wi[1][1]),
+                   "+v"(wq[2][1]), "+v"(wi[2][1]), "+v"(wq[3][1]), "+v"(wi[3][1])
+                 :: "memory");
   __syncthreads();
 
   // Epilogue through LDS, token-major: accumulator r of row tile a holds row
