@@ -23,20 +23,25 @@ def _x(orc, wk, seed, n, in_f, std=1.0):
     return dev_f16(wk, f16(orc, orc.fixture_normal(seed, 2, n * in_f, std)))
 
 
-@pytest.mark.parametrize("in_f,inter,n,exact", [(896, 4864, 256, True), (64, 33, 1, True),
-                                                (128, 4096, 300, True), (3584, 100, 37, False)])
-def test_gemm_swiglu_chunk_equals_gemm_then_swiglu(orc, wk, in_f, inter, n, exact):
+@pytest.mark.parametrize("in_f,inter,n,exact,step", [(896, 4864, 256, True, 256),
+                                                     (64, 33, 1, True, 256),
+                                                     (128, 4096, 300, True, 256),
+                                                     (3584, 100, 37, False, 256),
+                                                     (896, 16640, 512, True, 512)])
+def test_gemm_swiglu_chunk_equals_gemm_then_swiglu(orc, wk, in_f, inter, n, exact, step):
     """Bit for bit where the unfused GEMM runs unsplit (an output tile's sum in
     one K order). The fused form never splits K; where the unfused one does
-    (few output tiles: the last case), its f32 sums are added in another
-    order, and the f16 outputs may differ in the last place."""
+    (few output tiles: the fourth case), its f32 sums are added in another
+    order, and the f16 outputs may differ in the last place. The last case
+    runs 512 tokens in one call, as a batched prefill does: 260 x 2 tiles of
+    128 rows, so both forms take the 128-row wide tiles."""
     lin = _lin(orc, wk, 21, in_f, 2 * inter)
     x = _x(orc, wk, 22, n, in_f)
     gu = wk.DeviceBuffer(n * 2 * inter, np.float32)
     want = wk.DeviceBuffer(n * inter, np.float16)
     got = wk.DeviceBuffer(n * inter, np.float16)
-    for j in range(0, n, 256):  # chunks of at most 256 tokens, as the engine runs them
-        m = min(256, n - j)
+    for j in range(0, n, step):  # chunks of at most `step` tokens
+        m = min(step, n - j)
         xo = x.ptr.value + j * in_f * 2
         ffi.call("wst_gemm_int4_hier", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, xo, None, gu.ptr,
                  in_f, 2 * inter, m, 0)

@@ -481,7 +481,8 @@ def test_rescore_refuses_mismatched_shapes(orc, wk):
 
 
 @pytest.mark.parametrize("in_f,out_f,n,accum", [(896, 1152, 256, False), (3584, 520, 37, True),
-                                               (4864, 96, 130, False), (64, 9, 1, True)])
+                                               (4864, 96, 130, False), (64, 9, 1, True),
+                                               (896, 33000, 300, True)])
 def test_gemm_int4_hier_matches_dequantised_matmul(orc, wk, in_f, out_f, n, accum):
     """The MFMA chunk GEMM (f16 weight tiles, f32 accumulate) against float64
     dequant(W) @ x. Each weight is rounded to f16 once, so every output is

@@ -313,6 +313,16 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 //   issues 4 DMA ops and then 2 weight loads; x(st) is followed by exactly
 //   2 + 6 (GW_DX - 1) ops when step st is computed, so that vmcnt there
 //   covers x(st) and the weights of step st + 1, issued before it.
+// * Hazard of that scheme: the compiler takes an asm load's output register
+//   as written when the load issues, so it may copy or rename a ring
+//   register while its load is still landing. Each ring slot must keep its
+//   physical registers from the prologue through every loop round and the
+//   tail, as the shipped variants do (read off their ISA: the same eight or
+//   sixteen destination registers in every round). A 128-row variant (four
+//   accumulator tiles a wave, 168 VGPRs) broke this: one ring register was
+//   renamed across the loop's back edge and rows 96..127 of some tiles came
+//   out wrong (tests/test_gpu_kernels.py's 896 -> 33000 case caught it). It
+//   is not built.
 // * K advances two groups (64 columns) per step; split-K and the epilogue
 //   (through LDS, token-major) are those of gemm_mfma_kernel. SWI: rows
 //   0..31 of a tile are gate rows a0..a0+31 and rows 32..63 the up rows
