@@ -241,21 +241,47 @@ def golden_cfg2_ref():
 
 
 def golden_cfg4():
+    """The 4096-token prompt, then the configuration's 128 greedy tokens, from
+    the mirrored (f64-summing) oracle; with a sample of the first generated
+    step's logits (the top 64 and every 64th) and the distance between the
+    oracle's two f32 summation orders at that step (each runs the whole
+    prompt in its own order), so that a GPU stream's departure from this one
+    can be held to a margin two implementations that far apart could split."""
     t0 = time.time()
     cfg = dict(O.QWEN05B, qk_norm=1, rescore_k=32)
     n_prompt = 4096
     m = O.Model(cfg, SEED)
     prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt)
-    st = O.State(m, n_prompt + N_NEW_CFG4 + 8, 0)
-    for i, t in enumerate(prompt):
-        nxt, lg = st.step(int(t))
-        if i % 512 == 511:
-            print(f"cfg4 prompt {i + 1}/{n_prompt} ({time.time() - t0:.0f}s)", flush=True)
+
+    def run_prompt(tag):
+        st = O.State(m, n_prompt + N_NEW_CFG4 + 8, 0)
+        for i, t in enumerate(prompt):
+            nxt, lg = st.step(int(t))
+            if i % 512 == 511:
+                print(f"cfg4 {tag} prompt {i + 1}/{n_prompt} ({time.time() - t0:.0f}s)", flush=True)
+        return st, nxt, lg
+
+    drift = {}
+    for name, acc in (("f32_seq", O.ACC_F32_SEQ), ("f32_lane", O.ACC_F32_LANE)):
+        with O.variant(acc):
+            st, _, lg_v = run_prompt(name)
+            drift[name] = lg_v.astype(np.float64)
+            st.close()
+    st, nxt, lg = run_prompt("mirrored")
+    lg0 = lg.copy().astype(np.float64)
     tokens, margins, top = _decode(st, nxt, lg, N_NEW_CFG4)
+    top64 = np.argsort(-lg0, kind="stable")[:64]
+    sample = np.unique(np.concatenate([top64, np.arange(0, cfg["vocab"], 64)]))
     _write("qwen05b_qk_rescore_4096.json",
            dict(config="qwen2.5-0.5b-shape, qk_norm, rescore_k=32", seed=SEED,
                 prompt_seed=PROMPT_SEED, n_prompt=n_prompt, tokens=tokens, margins=margins,
-                top_logit=top, oracle="mirrored"), t0)
+                top_logit=top, oracle="mirrored",
+                first_step_logits=dict(index=[int(i) for i in sample],
+                                       value=[float(lg0[i]) for i in sample]),
+                first_step_order_drift=dict(
+                    f32_seq_vs_f32_lane=float(np.max(np.abs(drift["f32_seq"] - drift["f32_lane"]))),
+                    mirrored_vs_f32_seq=float(np.max(np.abs(lg0 - drift["f32_seq"]))),
+                    mirrored_vs_f32_lane=float(np.max(np.abs(lg0 - drift["f32_lane"]))))), t0)
 
 
 if __name__ == "__main__":

@@ -185,28 +185,45 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
   // the products (k ascending) is that of a plain K loop. (Measured against
   // running whole rounds of three steps, which keeps every wait partial but
   // multiplies up to two steps of zero weights: slower, 76k against 93k tok/s
-  // of config-4 prefill.)
+  // of config-4 prefill.) Whole rounds run in a loop with no exit inside it,
+  // the one or two remaining steps after it: with an exit after each step,
+  // the compiler moved the 16 accumulators between AGPRs every step (48
+  // v_accvgpr_mov a round).
   GmStage<HIER> S0, S1, S2;
   load(S0, 0);
   load(S1, 1);
   store(S0, 0, 0);
   __syncthreads();
-  for (int st = 0; st < steps; st += 3) {
-    load(S2, st + 2);
-    compute(S0, st & 1);
-    store(S1, st + 1, (st + 1) & 1);
-    __syncthreads();
-    if (st + 1 >= steps) break;
-    load(S0, st + 3);
-    compute(S1, (st + 1) & 1);
-    store(S2, st + 2, st & 1);
-    __syncthreads();
-    if (st + 2 >= steps) break;
-    load(S1, st + 4);
-    compute(S2, st & 1);
-    store(S0, st + 3, (st + 1) & 1);
-    __syncthreads();
+#define GM_STEP_A                      \
+  load(S2, st + 2);                    \
+  compute(S0, st & 1);                 \
+  store(S1, st + 1, (st + 1) & 1);     \
+  __syncthreads();
+#define GM_STEP_B                      \
+  load(S0, st + 3);                    \
+  compute(S1, (st + 1) & 1);           \
+  store(S2, st + 2, st & 1);           \
+  __syncthreads();
+#define GM_STEP_C                      \
+  load(S1, st + 4);                    \
+  compute(S2, st & 1);                 \
+  store(S0, st + 3, (st + 1) & 1);     \
+  __syncthreads();
+  int st = 0;
+  for (; st + 3 <= steps; st += 3) {
+    GM_STEP_A
+    GM_STEP_B
+    GM_STEP_C
   }
+  if (st < steps) {
+    GM_STEP_A
+  }
+  if (st + 1 < steps) {
+    GM_STEP_B
+  }
+#undef GM_STEP_A
+#undef GM_STEP_B
+#undef GM_STEP_C
 
   // Epilogue through LDS: C[row][token] (lane: rows 4*(lane/16)+i of each
   // 16-row tile, token lane%16) is stored token-major into the W buffers
