@@ -825,123 +825,116 @@ __global__ __launch_bounds__(512) void gemm_reduce_norm8_kernel(
 // cache). The QK-norm sum is the wave's sum, which is what a one-wave block's
 // block_sum returns (its second stage adds the one wave total to 0).
 //
-// A wave per (token, head) item, four waves a block (as fast as a 64-thread
-// block per item: 25 us over 4096 tokens x 18 heads, 38 MB; a wave taking
-// eight items, their loads all issued before the first rotation or only the
-// next item's ahead, 32-33 us).
-#define RR_WAVES 4
-#define RR_ITEMS 1
-struct RrIn {
-  float v[4];  // the item's reduced columns held by this lane
-  float c, s;  // its rotation factors
-};
+// A wave per token (a block each): it takes the token's heads RR_GROUP at a
+// time, issuing the group's loads (and the token's rotation factors, once)
+// before it rotates the first head. With a wave per (token, head) item the
+// kernel was bound by waves in flight: 73,728 short waves, each a memory
+// round trip (25.7 us over 4096 tokens x 18 heads with QK-norm, 38 MB; now
+// 21.4 us, 14.1 without QK-norm). NARROW: head_dim <= 64.
+#define RR_WAVES 1
+#define RR_GROUP 8
+template <bool NARROW>
 __global__ __launch_bounds__(64 * RR_WAVES) void gemm_reduce_rope_kernel(
     const float *__restrict__ ws, const uint16_t *__restrict__ bias, float *__restrict__ qkv,
     int splits, int n, uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache,
     const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, int n_q, int n_kv,
     int hd, int pos0, int max_seq, const uint16_t *__restrict__ q_norm_w,
     const uint16_t *__restrict__ k_norm_w, float eps) {
-  const int nh = n_q + n_kv, items = n * nh;
-  const int first = (blockIdx.x * RR_WAVES + (int)(threadIdx.x >> 6)) * RR_ITEMS;
-  if (first >= items) return;  // a whole wave: no barriers below
-  const int last = min(first + RR_ITEMS, items);
+  const int tok = blockIdx.x * RR_WAVES + (int)(threadIdx.x >> 6);
+  if (tok >= n) return;  // a whole wave: no barriers below
+  const int nh = n_q + n_kv;
   const int half = hd >> 1, j = threadIdx.x & 63;
   const int nqkv = (n_q + 2 * n_kv) * hd;
   const size_t total = (size_t)n * nqkv;
-  // Lane roles. half <= 32: one column per lane (lanes 0..31 the first half,
-  // 32..63 the second), the rotation partner over a cross-lane swap; else
-  // lane j < half holds columns j and j + half. The norm's sum and every
-  // product are the same in both forms.
-  const bool narrow = half <= 32;
-  const bool hi = narrow && j >= 32;
-  const int jj = narrow ? (j & 31) : j;
+  // Lane roles. NARROW (half <= 32): one column per lane (lanes 0..31 the
+  // first half, 32..63 the second), the rotation partner over a cross-lane
+  // swap; else lane j < half holds columns j and j + half. The norm's sum
+  // and every product are the same in both forms.
+  const bool hi = NARROW && j >= 32;
+  const int jj = NARROW ? (j & 31) : j;
   const bool act = jj < half;
   const int off = jj + (hi ? half : 0);
-  // column e of item (head) relative to the row: q heads use e = 0 (and 1
-  // in the wide form), kv heads k then v
-  auto col = [&](int head, int e) {
-    if (head < n_q) return head * hd + (narrow ? off : jj + e * half);
-    const int kvh = head - n_q;
+  constexpr int NV = NARROW ? 2 : 4;  // a kv head's columns per lane (k, then v)
+  // column e of head h relative to the row: q heads use e = 0 (and 1 in the
+  // wide form), kv heads k then v
+  auto col = [&](int h, int e) {
+    if (h < n_q) return h * hd + (NARROW ? off : jj + e * half);
+    const int kvh = h - n_q;
     const int k0 = (n_q + kvh) * hd, v0 = (n_q + n_kv + kvh) * hd;
-    if (narrow) return (e == 0 ? k0 : v0) + off;
+    if (NARROW) return (e == 0 ? k0 : v0) + off;
     return (e < 2 ? k0 : v0) + jj + (e & 1) * half;
   };
-  auto ncols = [&](int head) { return (head < n_q ? 1 : 2) * (narrow ? 1 : 2); };
-  auto fetch = [&](int it, RrIn &r) {
-    const int head = it % nh, tok = it / nh;
-    const float *wrow = ws + (size_t)tok * nqkv;
-    const int pos = min(max(pos0 + tok, 0), max_seq - 1);
-    const int nc = ncols(head);
+  auto ncols = [&](int h) { return (h < n_q ? 1 : 2) * (NARROW ? 1 : 2); };
+  const float *wrow = ws + (size_t)tok * nqkv;
+  float *row = qkv + (size_t)tok * nqkv;
+  const int pos = min(max(pos0 + tok, 0), max_seq - 1);
+  const float c = act ? cos_tab[(size_t)pos * half + jj] : 0.0f;
+  const float s = act ? sin_tab[(size_t)pos * half + jj] : 0.0f;
+  for (int h0 = 0; h0 < nh; h0 += RR_GROUP) {
+    float v[RR_GROUP][NV];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float t = 0.0f;
-      if (act && e < nc) {
-        const int c = col(head, e);
-        t = split_sum(wrow, c, total, splits);
-        if (bias) t += h2f(bias[c]);
+    for (int u = 0; u < RR_GROUP; ++u) {
+      const int h = h0 + u;
+#pragma unroll
+      for (int e = 0; e < NV; ++e) {
+        float t = 0.0f;
+        if (h < nh && act && e < ncols(h)) {
+          const int cc = col(h, e);
+          t = split_sum(wrow, cc, total, splits);
+          if (bias) t += h2f(bias[cc]);
+        }
+        v[u][e] = t;
       }
-      r.v[e] = t;
     }
-    r.c = act ? cos_tab[(size_t)pos * half + jj] : 0.0f;
-    r.s = act ? sin_tab[(size_t)pos * half + jj] : 0.0f;
-  };
-  RrIn in[RR_ITEMS];
 #pragma unroll
-  for (int k = 0; k < RR_ITEMS; ++k)
-    if (first + k < last) fetch(first + k, in[k]);
+    for (int u = 0; u < RR_GROUP; ++u) {
+      const int h = h0 + u;
+      if (h >= nh) break;  // uniform
+      const int nc = ncols(h);
+      if (act && h >= n_q) {  // k and v: the reduced values, as gemm_split_reduce_kernel
+                              // stores them (q's are overwritten below by their rotation)
 #pragma unroll
-  for (int k = 0; k < RR_ITEMS; ++k) {
-    const int it = first + k;
-    if (it >= last) break;
-    const RrIn &cur = in[k];
-    const int head = it % nh, tok = it / nh;
-    float *row = qkv + (size_t)tok * nqkv;
-    const int pos = min(max(pos0 + tok, 0), max_seq - 1);
-    const int nc = ncols(head);
-    if (act && head >= n_q) {  // k and v: the reduced values, as gemm_split_reduce_kernel
-                               // stores them (q's are overwritten below by their rotation)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (e < nc) row[col(head, e)] = cur.v[e];
-    }
-    const float c = cur.c, s = cur.s;
-    const bool is_q = head < n_q;
-    const uint16_t *__restrict__ g = is_q ? q_norm_w : k_norm_w;
-    if (narrow) {
-      const float mine = cur.v[0];
-      const float other = __shfl_xor(mine, 32);
-      float x1 = hi ? other : mine, x2 = hi ? mine : other;
-      if (g) {
-        const float ss = wave_sum(act && !hi ? fmaf(x1, x1, x2 * x2) : 0.0f);
-        const float sc = 1.0f / sqrtf(ss / (float)hd + eps);
+        for (int e = 0; e < NV; ++e)
+          if (e < nc) row[col(h, e)] = v[u][e];
+      }
+      const bool is_q = h < n_q;
+      const uint16_t *__restrict__ g = is_q ? q_norm_w : k_norm_w;
+      if constexpr (NARROW) {
+        const float mine = v[u][0];
+        const float other = __shfl_xor(mine, 32);
+        float x1 = hi ? other : mine, x2 = hi ? mine : other;
+        if (g) {
+          const float ss = wave_sum(act && !hi ? fmaf(x1, x1, x2 * x2) : 0.0f);
+          const float sc = 1.0f / sqrtf(ss / (float)hd + eps);
+          if (act) {
+            x1 = x1 * sc * h2f(g[jj]);
+            x2 = x2 * sc * h2f(g[jj + half]);
+          }
+        }
+        const float lo = rope_lo(x1, x2, c, s), hv = rope_hi(x1, x2, c, s);
         if (act) {
-          x1 = x1 * sc * h2f(g[jj]);
-          x2 = x2 * sc * h2f(g[jj + half]);
+          if (is_q) {
+            row[col(h, 0)] = hi ? hv : lo;
+          } else {
+            const size_t slot = ((size_t)(h - n_q) * max_seq + pos) * hd;
+            k_cache[slot + off] = f2h(hi ? hv : lo);
+            v_cache[slot + off] = f2h(v[u][1]);
+          }
         }
-      }
-      const float lo = rope_lo(x1, x2, c, s), hv = rope_hi(x1, x2, c, s);
-      if (act) {
-        if (is_q) {
-          row[col(head, 0)] = hi ? hv : lo;
-        } else {
-          const size_t slot = ((size_t)(head - n_q) * max_seq + pos) * hd;
-          k_cache[slot + off] = f2h(hi ? hv : lo);
-          v_cache[slot + off] = f2h(cur.v[1]);
-        }
-      }
-    } else {
-      float x1 = cur.v[0], x2 = cur.v[1];
-      if (g) qk_norm_wave(x1, x2, g, jj, half, hd, eps, act);
-      if (act) {
-        if (is_q) {
-          row[head * hd + jj] = rope_lo(x1, x2, c, s);
-          row[head * hd + jj + half] = rope_hi(x1, x2, c, s);
-        } else {
-          const size_t slot = ((size_t)(head - n_q) * max_seq + pos) * hd;
-          k_cache[slot + jj] = f2h(rope_lo(x1, x2, c, s));
-          k_cache[slot + jj + half] = f2h(rope_hi(x1, x2, c, s));
-          v_cache[slot + jj] = f2h(cur.v[2]);
-          v_cache[slot + jj + half] = f2h(cur.v[3]);
+      } else {
+        float x1 = v[u][0], x2 = v[u][1];
+        if (g) qk_norm_wave(x1, x2, g, jj, half, hd, eps, act);
+        if (act) {
+          if (is_q) {
+            row[h * hd + jj] = rope_lo(x1, x2, c, s);
+            row[h * hd + jj + half] = rope_hi(x1, x2, c, s);
+          } else {
+            const size_t slot = ((size_t)(h - n_q) * max_seq + pos) * hd;
+            k_cache[slot + jj] = f2h(rope_lo(x1, x2, c, s));
+            k_cache[slot + jj + half] = f2h(rope_hi(x1, x2, c, s));
+            v_cache[slot + jj] = f2h(v[u][2]);
+            v_cache[slot + jj + half] = f2h(v[u][3]);
+          }
         }
       }
     }
@@ -1239,11 +1232,17 @@ extern "C" wst_status_t wst_gemm_hier_rope_chunks(const void *qw, const void *si
   int splits;
   st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits, plan_n);
   if (st != WST_OK) return st;
-  const int rr_waves = ((n_q + n_kv) * n + RR_ITEMS - 1) / RR_ITEMS;
-  gemm_reduce_rope_kernel<<<(rr_waves + RR_WAVES - 1) / RR_WAVES, 64 * RR_WAVES, 0, WST_STREAM>>>(
-      ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,
-      (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv, head_dim,
-      pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
+  const dim3 rr_grid((n + RR_WAVES - 1) / RR_WAVES);
+  if (head_dim <= 64)
+    gemm_reduce_rope_kernel<true><<<rr_grid, 64 * RR_WAVES, 0, WST_STREAM>>>(
+        ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,
+        (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv, head_dim,
+        pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
+  else
+    gemm_reduce_rope_kernel<false><<<rr_grid, 64 * RR_WAVES, 0, WST_STREAM>>>(
+        ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,
+        (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv, head_dim,
+        pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
   WST_TRY_KERNEL("wst_gemm_hier_rope_chunk");
   return WST_OK;
 }
