@@ -9,10 +9,13 @@ The reference's contract for this path (crates/whetstone-core/src/engine.rs:
 195-199): chunked prefill gives the same greedy output as sequential prefill.
 The first token after a chunked prefill comes from the chunk pass's own head,
 the plain int4 GEMM without the fp16 rescore (engine.rs:824-835); after a
-sequential prefill and at every decode step the top 32 logits are rescored
-from the fp16 head copy. So the first step's logit vectors differ by the
-head's int4 error on the rescored entries (~0.17 here) by design, and the
-later steps by the prefill forms' rounding only.
+sequential prefill and at every decode step the leading logits (those above
+the rescore ladder's threshold: at least 32, about 300 on these weights) are
+recomputed from the fp16 head copy. So the first step's logit vectors differ
+by the head's int4 error on the rescored entries (~0.14 here) by design;
+with the rescore off the two prefill forms' first-step logits are 0.007
+apart at 256 to 4096 tokens. At the later steps both are rescored, and an
+entry near the threshold can still be rescored in one and not the other.
 
 Two implementations whose logits differ by at most d can pick different
 tokens only where a top-2 margin is below 2 d; so each comparison holds the
