@@ -144,3 +144,26 @@ def test_stream_after_4096_prompt_matches_oracle(streams, chunked):
         print(f"  step {k}: {toks[k]} vs the oracle's {want[k]}, its top-2 margin "
               f"{margins[k]:.4g}, bound {bound:.4g}")
         assert margins[k] < bound, (k, margins[k], bound)
+
+
+def test_prefill_forms_agree_without_the_rescore():
+    """The same model with the head rescore off, so that both prefill forms
+    end on the plain int4 head: their first-step logits after the 4096-token
+    prompt are within the north star's 1e-2 + 1e-3 |ref| of each other
+    everywhere (measured 0.007), and pick the same token."""
+    g = E.Model(dict(CFG, rescore_k=0), seed=GOLDEN["seed"])
+    prompt = np.random.default_rng(GOLDEN["prompt_seed"]).integers(
+        0, CFG["vocab"], GOLDEN["n_prompt"]).astype(np.int32)
+    out = {}
+    for chunked in (True, False):
+        print(f"config 4 without rescore: {'chunked' if chunked else 'sequential'} prefill",
+              flush=True)
+        eng = E.Engine(g, GOLDEN["n_prompt"] + 8)
+        eng.prefill(prompt, chunked=chunked)
+        out[chunked] = (eng.logits(), eng.token())
+        eng.close()
+    g.close()
+    d = float(np.max(np.abs(out[True][0].astype(np.float64) - out[False][0])))
+    print(f"  first-step logits {d:.4g} apart")
+    assert np.allclose(out[True][0], out[False][0], rtol=1e-3, atol=1e-2), d
+    assert out[True][1] == out[False][1] or _top2(out[False][0]) < 2 * d
