@@ -825,24 +825,26 @@ __global__ __launch_bounds__(512) void gemm_reduce_norm8_kernel(
 // cache). The QK-norm sum is the wave's sum, which is what a one-wave block's
 // block_sum returns (its second stage adds the one wave total to 0).
 //
-// A wave per token (a block each): it takes the token's heads RR_GROUP at a
-// time, issuing the group's loads (and the token's rotation factors, once)
-// before it rotates the first head. With a wave per (token, head) item the
-// kernel was bound by waves in flight: 73,728 short waves, each a memory
-// round trip (25.7 us over 4096 tokens x 18 heads with QK-norm, 38 MB; now
-// 21.4 us, 14.1 without QK-norm). NARROW: head_dim <= 64.
+// A wave (a block) per token and group of RR_GROUP heads: it issues the
+// group's loads and the token's rotation factors before it rotates the first
+// head. With a wave per (token, head) item the kernel was bound by waves in
+// flight: 73,728 short waves, each a memory round trip (25.7 us over 4096
+// tokens x 18 heads with QK-norm, 38 MB; now 21.4 us, 14.1 without QK-norm).
+// Over one 256-token chunk (the qkv sum split over K there) groups of eight
+// leave too few waves: 9.8 us against 4.3 for a wave per head, so below 1024
+// tokens a group is one head. NARROW: head_dim <= 64.
 #define RR_WAVES 1
-#define RR_GROUP 8
-template <bool NARROW>
+template <bool NARROW, int RR_GROUP>
 __global__ __launch_bounds__(64 * RR_WAVES) void gemm_reduce_rope_kernel(
     const float *__restrict__ ws, const uint16_t *__restrict__ bias, float *__restrict__ qkv,
     int splits, int n, uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache,
     const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, int n_q, int n_kv,
     int hd, int pos0, int max_seq, const uint16_t *__restrict__ q_norm_w,
     const uint16_t *__restrict__ k_norm_w, float eps) {
-  const int tok = blockIdx.x * RR_WAVES + (int)(threadIdx.x >> 6);
-  if (tok >= n) return;  // a whole wave: no barriers below
-  const int nh = n_q + n_kv;
+  const int nh = n_q + n_kv, ngrp = (nh + RR_GROUP - 1) / RR_GROUP;
+  const int item = blockIdx.x * RR_WAVES + (int)(threadIdx.x >> 6);
+  if (item >= n * ngrp) return;  // a whole wave: no barriers below
+  const int tok = item / ngrp, grp = item % ngrp;
   const int half = hd >> 1, j = threadIdx.x & 63;
   const int nqkv = (n_q + 2 * n_kv) * hd;
   const size_t total = (size_t)n * nqkv;
@@ -870,7 +872,8 @@ __global__ __launch_bounds__(64 * RR_WAVES) void gemm_reduce_rope_kernel(
   const int pos = min(max(pos0 + tok, 0), max_seq - 1);
   const float c = act ? cos_tab[(size_t)pos * half + jj] : 0.0f;
   const float s = act ? sin_tab[(size_t)pos * half + jj] : 0.0f;
-  for (int h0 = 0; h0 < nh; h0 += RR_GROUP) {
+  {
+    const int h0 = grp * RR_GROUP;
     float v[RR_GROUP][NV];
 #pragma unroll
     for (int u = 0; u < RR_GROUP; ++u) {
@@ -1016,16 +1019,20 @@ GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0, b
   // (The wide tiles address x with 32-bit byte offsets.)
   p.wide = hier && wide_tiles() && in_f >= GW_KC && (in_f >= 2048 || rows >= 4096) &&
            (size_t)n * in_f * 2 < ((size_t)1 << 31);
-  // Wide tiles of 128 tokens for the split-K shapes, where 256-token tiles
-  // would leave CUs without a tile: 7B qkv 43.0 -> 36.2 us, 7B down 100.3 ->
-  // 95.6 us (0.5B down unchanged). Not for the SwiGLU form, which never
-  // splits: its 128-token tiles run one wave per SIMD (0.5B gate|up 14.0 ->
-  // 16.7 us). WST_GEMM_BN=128|256 forces one.
+  // Wide tiles of 128 tokens for the split-K shapes (256-token tiles fewer
+  // than half the CUs), where 256-token tiles would leave CUs without a
+  // tile: 7B qkv 43.0 -> 36.2 us, 7B down 100.3 -> 95.6 us (0.5B down
+  // unchanged). Not where the 256-token tiles already fill about one round
+  // of the CUs without splitting (the 0.5B down over a 4096-token batched
+  // prefill, 224 tiles: 76.2 -> 65.2 us), nor for the SwiGLU form, which
+  // never splits: its 128-token tiles run one wave per SIMD (0.5B gate|up
+  // 14.0 -> 16.7 us). WST_GEMM_BN=128|256 forces one.
   p.nwv = 8;
   if (p.wide) {
     const int forced = gemm_bn_override();
     const int t256 = ((out_f + GW_BM - 1) / GW_BM) * ((pn + 255) / 256);
-    if (forced == 128 || (forced != 256 && !swi && pn > 128 && t256 < wst_cu_count())) p.nwv = 4;
+    if (forced == 128 || (forced != 256 && !swi && pn > 128 && t256 < wst_cu_count() / 2))
+      p.nwv = 4;
   }
   p.bm = p.wide ? GW_BM : GM_BM;
   p.bn = p.wide ? 32 * p.nwv : GM_BN;
@@ -1232,17 +1239,24 @@ extern "C" wst_status_t wst_gemm_hier_rope_chunks(const void *qw, const void *si
   int splits;
   st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits, plan_n);
   if (st != WST_OK) return st;
-  const dim3 rr_grid((n + RR_WAVES - 1) / RR_WAVES);
-  if (head_dim <= 64)
-    gemm_reduce_rope_kernel<true><<<rr_grid, 64 * RR_WAVES, 0, WST_STREAM>>>(
-        ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,
-        (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv, head_dim,
-        pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
-  else
-    gemm_reduce_rope_kernel<false><<<rr_grid, 64 * RR_WAVES, 0, WST_STREAM>>>(
-        ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,
-        (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv, head_dim,
-        pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps);
+#define RR_LAUNCH(NARROW_, G_)                                                                 \
+  do {                                                                                       \
+    const int items_ = n * ((n_q + n_kv + (G_) - 1) / (G_));                                 \
+    gemm_reduce_rope_kernel<NARROW_, G_><<<(items_ + RR_WAVES - 1) / RR_WAVES, 64 * RR_WAVES, 0, \
+                                           WST_STREAM>>>(                                    \
+        ws, (const uint16_t *)bias, (float *)qkv, splits, n, (uint16_t *)k_cache,            \
+        (uint16_t *)v_cache, (const float *)cos_tab, (const float *)sin_tab, n_q, n_kv,       \
+        head_dim, pos0, max_seq, (const uint16_t *)q_norm_w, (const uint16_t *)k_norm_w, eps); \
+  } while (0)
+  const bool big = n >= 1024;
+  if (head_dim <= 64) {
+    if (big) RR_LAUNCH(true, 8);
+    else RR_LAUNCH(true, 1);
+  } else {
+    if (big) RR_LAUNCH(false, 8);
+    else RR_LAUNCH(false, 1);
+  }
+#undef RR_LAUNCH
   WST_TRY_KERNEL("wst_gemm_hier_rope_chunk");
   return WST_OK;
 }
