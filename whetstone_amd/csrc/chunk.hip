@@ -141,8 +141,8 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
 //   a 128-byte row per eight lanes) into row-major LDS tiles; the next tile's
 //   loads are issued before the current tile's softmax.
 // * P^T never goes through LDS: the score accumulators, exponentiated and
-//   split into f16 hi and lo parts, are the B operand of O^T = V^T . P^T as
-//   they stand, the MFMA's K index k = 8 kg + j standing for key 4 kg + j
+//   rounded to f16, are the B operand of O^T = V^T . P^T as they stand, the
+//   MFMA's K index k = 8 kg + j standing for key 4 kg + j
 //   (j < 4) and 16 + 4 kg + j - 4 (j >= 4); the V^T operand is gathered in
 //   that key order by the gfx950 transposing LDS read (ds_read_b64_tr_b16:
 //   within 16 lanes, lane L's element i comes from lane 4i + L/4's element
@@ -152,6 +152,14 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
 //   f32, and O's rescale is rare instead of taken on almost every tile by
 //   some token of the wave's. Softmax is exact for any reference point; only
 //   roundings move.
+// * P in one f16 (round to nearest, relative error <= 2^-11 per weight,
+//   averaging over the keys) where q keeps its hi + lo parts: a score error
+//   is an exponent error, a P error only a weight error, and the output is
+//   rounded to f16 (2^-11) anyway. With P as f16 hi + lo too
+//   (WST_ATTN_CHUNK_PLO=1, twice the P.V MFMAs and ~40 more VALU a tile)
+//   0.5B 4096 tokens took 88.5 against 75.1 us, 7B 367 against 317 us, and
+//   the chunked prefill's logits moved by nothing measurable (0.0068 and
+//   0.0065 from the sequential prefill's, rescore off).
 // Causality is a mask: token j keeps positions <= pos0 + j.
 //
 // A token's result does not depend on TG: its valid keys fall in the same
@@ -159,11 +167,11 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
 // wholly masked for it: no term and no rescale), so TG is picked by the token
 // count alone (WST_ATTN_CHUNK_TG=1|2 forces one).
 //
-// Measured (0.5B shape, 14/2 heads of 64, 4096 tokens from position 0): 87 us
-// (344 TFLOP/s causal) with TG 2; TG 1 106 us. The untransposed form (scores
-// S = q . K^T, P through LDS, a row spread over 16 lanes, O's accumulators in
-// AGPRs) took 142-187 us; K operands loaded straight from the cache instead
-// of through LDS, 113-160 us.
+// Measured (0.5B shape, 14/2 heads of 64, 4096 tokens from position 0): 75 us
+// (400 TFLOP/s causal) with TG 2 (with P as hi + lo: 87 us; TG 1 106 us).
+// The untransposed form (scores S = q . K^T, P through LDS, a row spread
+// over 16 lanes, O's accumulators in AGPRs) took 142-187 us; K operands
+// loaded straight from the cache instead of through LDS, 113-160 us.
 typedef _Float16 ac_h8 __attribute__((ext_vector_type(8)));
 typedef short ac_s4 __attribute__((ext_vector_type(4)));
 typedef float ac_f4 __attribute__((ext_vector_type(4)));
@@ -201,7 +209,7 @@ __device__ __forceinline__ float row4_max(float v) {  // over the lanes r16 + 16
   return __builtin_elementwise_maximum(p.a, p.b);
 }
 
-template <int HD, int TG>
+template <int HD, int TG, bool PLO = true>
 __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
     const float *__restrict__ qkv, const uint16_t *__restrict__ k_cache,
     const uint16_t *__restrict__ v_cache, uint16_t *__restrict__ out, int n_q, int n_kv,
@@ -349,18 +357,23 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
       float pv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(sc[g][j >> 2][j & 3] - mref);
-      // P^T hi and lo as B operands (k = 8kg + j <-> key, above); the hi
-      // parts converted in pairs
+      // P^T as the B operand (k = 8kg + j <-> key, above): one f16 each, or
+      // (PLO) hi parts converted in pairs and lo parts
       float psum = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
         psum += pv[j];
         psum += pv[j + 1];
-        const auto h2 = __builtin_amdgcn_cvt_pkrtz(pv[j], pv[j + 1]);
-        pbh[g][j] = h2[0];
-        pbh[g][j + 1] = h2[1];
-        pbl[g][j] = (_Float16)(pv[j] - (float)h2[0]);
-        pbl[g][j + 1] = (_Float16)(pv[j + 1] - (float)h2[1]);
+        if constexpr (PLO) {
+          const auto h2 = __builtin_amdgcn_cvt_pkrtz(pv[j], pv[j + 1]);
+          pbh[g][j] = h2[0];
+          pbh[g][j + 1] = h2[1];
+          pbl[g][j] = (_Float16)(pv[j] - (float)h2[0]);
+          pbl[g][j + 1] = (_Float16)(pv[j + 1] - (float)h2[1]);
+        } else {
+          pbh[g][j] = (_Float16)pv[j];
+          pbh[g][j + 1] = (_Float16)pv[j + 1];
+        }
       }
       l[g] = l[g] * corr[g] + psum;
       m[g] = mn;
@@ -388,7 +401,8 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
 #pragma unroll
       for (int g = 0; g < TG; ++g) {
         o[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbh[g], o[g][t], 0, 0, 0);
-        o[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbl[g], o[g][t], 0, 0, 0);
+        if constexpr (PLO)
+          o[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbl[g], o[g][t], 0, 0, 0);
       }
     }
     kt += AC_WAVES;
@@ -429,20 +443,32 @@ __global__ __launch_bounds__(AC_WAVES * 64) void attn_chunk_mfma_kernel(
   }
 }
 
-template <int HD, int TG>
-static void attn_chunk_mfma_tg(const void *qkv, const void *k_cache, const void *v_cache,
-                               void *out, int n_q, int n_kv, int pos0, int n, int max_seq,
-                               float scale) {
+template <int HD, int TG, bool PLO>
+static void attn_chunk_mfma_tgp(const void *qkv, const void *k_cache, const void *v_cache,
+                                void *out, int n_q, int n_kv, int pos0, int n, int max_seq,
+                                float scale) {
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void *)attn_chunk_mfma_kernel<HD, TG>,
+    (void)hipFuncSetAttribute((const void *)attn_chunk_mfma_kernel<HD, TG, PLO>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, AcShape<HD, TG>::LDS);
     attr = true;
   }
   const dim3 grid(n_q, (n + 16 * TG - 1) / (16 * TG));
-  attn_chunk_mfma_kernel<HD, TG><<<grid, AC_WAVES * 64, AcShape<HD, TG>::LDS, WST_STREAM>>>(
+  attn_chunk_mfma_kernel<HD, TG, PLO><<<grid, AC_WAVES * 64, AcShape<HD, TG>::LDS, WST_STREAM>>>(
       (const float *)qkv, (const uint16_t *)k_cache, (const uint16_t *)v_cache, (uint16_t *)out,
       n_q, n_kv, pos0, n, max_seq, scale);
+}
+template <int HD, int TG>
+static void attn_chunk_mfma_tg(const void *qkv, const void *k_cache, const void *v_cache,
+                               void *out, int n_q, int n_kv, int pos0, int n, int max_seq,
+                               float scale) {
+  const char *v = getenv("WST_ATTN_CHUNK_PLO");  // 1: P as f16 hi + lo
+  if (v && v[0] == '1')
+    attn_chunk_mfma_tgp<HD, TG, true>(qkv, k_cache, v_cache, out, n_q, n_kv, pos0, n, max_seq,
+                                      scale);
+  else
+    attn_chunk_mfma_tgp<HD, TG, false>(qkv, k_cache, v_cache, out, n_q, n_kv, pos0, n, max_seq,
+                                       scale);
 }
 
 // Two groups of 16 tokens per wave from 512 tokens up (0.5B shape, 4096
