@@ -76,7 +76,8 @@ def log(msg: str) -> None:
 def parse():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=256)
+    p.add_argument("--steps", type=int, default=None,
+                   help="timed decode steps (default 256; config 4: its 128 decode steps)")
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--config", type=int, default=3, choices=(0, 1, 2, 3, 4))
     p.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -114,7 +115,10 @@ def parse():
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run the counter calibration: a device-to-device copy, a "
                         "memset and a read sweep of MIB MiB each, then exit")
-    return p.parse_args()
+    a = p.parse_args()
+    if a.steps is None:
+        a.steps = 128 if a.config == 4 else 256
+    return a
 
 
 def _short(name: str) -> str:
