@@ -75,3 +75,13 @@ def assert_streams(got, want, margins, tie_margin=1e-4):
     k = next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
     assert margins[k] < tie_margin, f"diverged at step {k}: {got[k]} vs {want[k]}, margin {margins[k]}"
     return k
+
+
+def ns_tol(logits) -> float:
+    """The north star's logit tolerance as one number for a vector: 1e-2
+    max-abs plus 1e-3 of its largest magnitude. Two implementations within
+    it of each other can pick different greedy tokens only where a top-2
+    margin is below twice it. (Twice the measured distance between two
+    vectors bounds their own argmax flip by construction, so it tests
+    nothing; this bound is fixed before the run.)"""
+    return 1e-2 + 1e-3 * float(np.max(np.abs(np.asarray(logits, np.float64))))
