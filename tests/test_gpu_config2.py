@@ -50,7 +50,9 @@ def test_05b_ctx512_stream_matches_golden(chunked):
     k = _first_divergence(got, want)
     delta = GOLDEN["first_step_order_drift"]["f32_seq_vs_f32_lane"]
     print(f"0.5B ctx 512 ({'chunked' if chunked else 'sequential'} prefill): first {k}/{N_NEW} "
-          f"tokens identical to the oracle (order-only drift {delta:.4g})")
+          f"tokens identical to the oracle (order-only drift {delta:.4g}"
+          + (f"; the reference's own arithmetic is {GOLDEN['ref']['first_step_vs_f64']:.4g} "
+             f"from the oracle at the first step" if "ref" in GOLDEN else "") + ")")
     if k < N_NEW:
         assert margins[k] < 2 * max(delta, 1e-4), (
             f"diverged at step {k}: {got[k]} vs {want[k]}, oracle top-2 margin {margins[k]:.4g}")
