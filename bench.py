@@ -37,8 +37,10 @@ tokens, on the host) beside the GPU engine on the same weights.
 cold past the MALL and hot) and prints a line of its own.
 `--config 4` instead measures the chunked prefill (0.5B shape with QK-norm and
 the int4 head rescored from an fp16 copy, top-32): a 4096-token seeded prompt
-in 256-token chunks through the MFMA GEMMs, then 128 greedy decode steps, and
-prints a line of its own (prefill tok/s and achieved TFLOP/s, decode tok/s).
+in 256-token chunks through the MFMA GEMMs, the 16 chunks batched one launch
+per op and layer (and, for comparison, one launch per chunk and op), then 128
+greedy decode steps, and prints a line of its own (prefill tok/s and achieved
+TFLOP/s, decode tok/s). `--batched-only` skips the per-chunk timing.
 """
 import argparse
 import json
