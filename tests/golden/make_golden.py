@@ -284,9 +284,47 @@ def golden_cfg4():
                     mirrored_vs_f32_lane=float(np.max(np.abs(lg0 - drift["f32_lane"]))))), t0)
 
 
+def golden_7b_prompt():
+    """The 7B shape after a seeded 256-token prompt (one chunk): the f64-
+    summing oracle's first-step logits (a sample: the top 64 and every 64th)
+    and first token, and the same step in ORC_ACC_REF, the reference CUDA
+    build's own arithmetic, with its distance from the f64 oracle; for the
+    chunk path's parity at full depth."""
+    t0 = time.time()
+    cfg = O.QWEN7B
+    n_prompt = 256
+    m = O.Model(cfg, SEED)
+    prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg["vocab"], n_prompt)
+    lg = {}
+    for name, acc in (("f64", O.ACC_F64), ("ref", O.ACC_REF)):
+        with O.variant(acc):
+            st = O.State(m, n_prompt + 8, 0)
+            for i, t in enumerate(prompt):
+                nxt, l_ = st.step(int(t))
+                if i % 64 == 63:
+                    print(f"7b prompt {name} {i + 1}/{n_prompt} ({time.time() - t0:.0f}s)", flush=True)
+            lg[name] = (int(nxt), l_.astype(np.float64))
+            st.close()
+    l0 = lg["f64"][1]
+    top64 = np.argsort(-l0, kind="stable")[:64]
+    sample = np.unique(np.concatenate([top64, np.arange(0, cfg["vocab"], 64)]))
+    out = dict(config="qwen2.5-7b-shape", seed=SEED, prompt_seed=PROMPT_SEED, n_prompt=n_prompt,
+               first_token=lg["f64"][0], top2_margin=O.top2_margin(l0),
+               first_step_logits=dict(index=[int(i) for i in sample],
+                                      value=[float(l0[i]) for i in sample]),
+               ref=dict(sms=30, first_token=lg["ref"][0],
+                        first_step_vs_f64=float(np.max(np.abs(lg["ref"][1] - l0)))),
+               oracle="mirrored", threads=O.lib().orc_threads(),
+               seconds=round(time.time() - t0, 1))
+    path = HERE / "qwen7b_prompt256.json"
+    path.write_text(json.dumps(out, indent=1))
+    print(f"wrote {path} in {time.time() - t0:.1f}s; ref vs f64 {out['ref']['first_step_vs_f64']:.4f}",
+          flush=True)
+
+
 if __name__ == "__main__":
     which = sys.argv[1:] or ["05b"]
     for w in which:
         {"05b": golden_05b, "7b": golden_7b, "7bref": golden_7b_ref, "cfg2": golden_cfg2,
          "cfg2ref": golden_cfg2_ref,
-         "cfg4": golden_cfg4}[w]()
+         "cfg4": golden_cfg4, "7bprompt": golden_7b_prompt}[w]()

@@ -174,3 +174,38 @@ def test_7b_greedy_stream_matches_golden(model7b):
         assert ref["margins"][kr] < bound, (
             f"diverged from the reference arithmetic at step {kr}: its top-2 margin "
             f"{ref['margins'][kr]:.4g} >= {bound:.4g}")
+
+
+_PROMPT_PATH = Path(__file__).resolve().parent / "golden" / "qwen7b_prompt256.json"
+
+
+def test_7b_prefill_forms_against_oracle(model7b):
+    """The 7B shape after a seeded 256-token prompt, prefilled as one chunk
+    (MFMA GEMMs with f16 weight tiles, chunk attention) and token by token
+    (the decode step), against the f64-summing oracle's first-step logits
+    (tests/golden/qwen7b_prompt256.json: a sample of them, the top 64 and
+    every 64th). At this depth the reference's own arithmetic (ORC_ACC_REF)
+    is the golden file's `ref.first_step_vs_f64` from the oracle; both
+    prefill forms are held to be at least as close, and to pick the oracle's
+    token unless its top-2 margin is below twice that distance."""
+    if not _PROMPT_PATH.exists():
+        pytest.fail(f"{_PROMPT_PATH.name} is missing: python tests/golden/make_golden.py 7bprompt")
+    gold = json.loads(_PROMPT_PATH.read_text())
+    assert gold["seed"] == GOLDEN["seed"]
+    prompt = np.random.default_rng(gold["prompt_seed"]).integers(
+        0, E.QWEN7B["vocab"], gold["n_prompt"]).astype(np.int32)
+    idx = np.asarray(gold["first_step_logits"]["index"])
+    want = np.asarray(gold["first_step_logits"]["value"], np.float64)
+    ref_dist = gold["ref"]["first_step_vs_f64"]
+    for chunked in (True, False):
+        eng = E.Engine(model7b, gold["n_prompt"] + 8)
+        eng.prefill(prompt, chunked=chunked)
+        got, tok = eng.logits().astype(np.float64), eng.token()
+        eng.close()
+        d = float(np.max(np.abs(got[idx] - want)))
+        print(f"7B after a {gold['n_prompt']}-token prompt, {'chunked' if chunked else 'sequential'} "
+              f"prefill: {d:.4f} from the f64 oracle on its sample (the reference's arithmetic "
+              f"{ref_dist:.4f}); token {tok} (oracle {gold['first_token']}, top-2 margin "
+              f"{gold['top2_margin']:.4g})")
+        assert d <= ref_dist, (chunked, d, ref_dist)
+        assert tok == gold["first_token"] or gold["top2_margin"] < 2 * ref_dist
