@@ -27,7 +27,8 @@ pytestmark = pytest.mark.gpu
 
 CFGS = {"05b_qk_rescore": dict(E.QWEN05B, qk_norm=1, rescore_k=32), "05b": E.QWEN05B,
         "7b": dict(E.QWEN7B, n_layers=4)}
-CASES = [("05b_qk_rescore", 1024), ("05b_qk_rescore", 900), ("05b", 768), ("7b", 512)]
+CASES = [("05b_qk_rescore", 1024), ("05b_qk_rescore", 900), ("05b", 768), ("05b", 769),
+         ("7b", 512)]
 
 
 def _run(g, prompt, n_new, mode):
