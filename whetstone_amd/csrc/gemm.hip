@@ -312,7 +312,10 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 //   word (8 weights) per step into the LDS W tile, as w = q * s + m in one f32
 //   fma -- q * s is exact in f32 (a 4-bit integer times an f16 times a 4-bit
 //   integer), so the single rounding equals the quantiser's two -- rounded to
-//   f16. The tile is double-buffered, one barrier per step.
+//   f16. On the 256-token tiles each W tile is dequantised two steps before
+//   its use into one of four LDS buffers, with a barrier after every other
+//   step (config-4 prefill 450-456k -> 461-465k tok/s; bit-identical); the
+//   128-token tiles keep two buffers and a barrier per step.
 // * x goes memory -> LDS by DMA (global_load_lds_dwordx4: 16 bytes per lane
 //   land at M0 + 16 * lane), three steps in flight in an LDS ring, with no
 //   registers held for it. Each wave loads only its own 32 tokens (a
@@ -327,9 +330,12 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 // * Every load of the loop is issued by inline asm with the wait counted by
 //   hand: left to itself the compiler sank each step's loads down to their
 //   first use, one step later, leaving one step in flight. Per step a thread
-//   issues 4 DMA ops and then 2 weight loads; x(st) is followed by exactly
-//   2 + 6 (GW_DX - 1) ops when step st is computed, so that vmcnt there
-//   covers x(st) and the weights of step st + 1, issued before it.
+//   issues 4 DMA ops and then 2 weight loads (x(q) just before the weights
+//   of step q + 2). When step st is computed, the wait lets through only the
+//   ops issued after the later of x(st) and the weights it dequantises next
+//   (GwShape::VMCNT: 12 on the 256-token tiles, whose next weights are
+//   step st + 2's, issued after x(st); 20 on the 128-token tiles, whose next
+//   weights are step st + 1's, issued before x(st)).
 // * Hazard of that scheme: the compiler takes an asm load's output register
 //   as written when the load issues, so it may copy or rename a ring
 //   register while its load is still landing. Each ring slot must keep its
@@ -355,7 +361,6 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 #define GW_DW 4                         // packed-weight steps in flight (registers)
 #define GW_XPAD 64                      // bytes between DMA blocks: t and t+8 on other banks
 #define GW_XWAVE (4 * (1024 + GW_XPAD)) // bytes of a wave's 32 tokens in one stage
-#define GW_LDS_W (2 * GW_WT * 2)
 static_assert(GW_DW == GW_DX + 1, "the wait count assumes the weights lead x by one step");
 
 // NWV waves of 32 tokens: 256-token tiles (8 waves, one packed word per
@@ -368,12 +373,23 @@ struct GwShape {
   static constexpr int RPT = 512 / THREADS;           // W words per thread per step
   static constexpr int XSTAGE = NWV * GW_XWAVE;       // bytes of one x ring stage
   static constexpr int LDS_X = GW_DX * XSTAGE;
+  // Steps ahead that W is dequantised into LDS: 2 for the 256-token tiles
+  // (four W buffers, a barrier every two steps), 1 for the 128-token ones
+  // (two buffers, a barrier every step: with the weights two steps ahead the
+  // compiler renamed a register of their load ring across the loop's back
+  // edge).
+  static constexpr int WA = NWV == 8 ? 2 : 1;
+  static constexpr int WB = 2 * WA;                   // W tile buffers
+  static constexpr int LDS_W = WB * GW_WT * 2;
   static constexpr int LDS_C = BN * GW_CS * 4;
-  static constexpr int LDS = LDS_X + GW_LDS_W > LDS_C ? LDS_X + GW_LDS_W : LDS_C;
-  // Ops issued after x(st) when step st is multiplied: x and W of the steps
-  // in flight (4 DMA ops and 2 RPT weight loads per step).
-  static constexpr int VMCNT = 4 * (GW_DX - 1) + 2 * RPT * GW_DX;
+  static constexpr int LDS = LDS_X + LDS_W > LDS_C ? LDS_X + LDS_W : LDS_C;
+  // Ops issued after the later of x(st) and W(st + WA) when step st is
+  // multiplied (4 DMA ops and 2 RPT weight loads per step, x(q) issued just
+  // before W(q + 2)): WA = 1, after x(st): W(st + 2) and the two steps
+  // since; WA = 2, after W(st + 2): the two steps since.
+  static constexpr int VMCNT = 4 * (GW_DX - 1) + 2 * RPT * (GW_DX + 1 - WA);
   static_assert(RPT * THREADS == 512, "64 rows x 2 groups x 4 words per step");
+  static_assert(LDS <= 160 * 1024, "one CU's LDS");
 };
 
 typedef float gm_f16v __attribute__((ext_vector_type(16)));
@@ -435,6 +451,10 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
   const uint32_t wave_x = lds0 + (uint32_t)wave * GW_XWAVE;
 
   auto issue_x = [&](int step) {  // 4 DMA ops
+    // The stage was last read by this wave's own step - GW_DX: its LDS reads
+    // must be complete before the DMA can land (with a barrier after every
+    // step, its fence waited for them).
+    if constexpr (S::WA == 2) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     step = min(step, steps - 1);
     const int col = min((g_begin + step * GW_KG) * HGROUP, in_f - GW_KC);
     const uint32_t stage = wave_x + (uint32_t)(step % GW_DX) * S::XSTAGE;
@@ -496,7 +516,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
   // token l32 sits in DMA block l32 / 8, row l32 % 8
   const uint32_t xrow0 = (uint32_t)(l32 >> 3) * (1024u + GW_XPAD) + (uint32_t)(l32 & 7) * 128u;
   auto compute = [&](int step) {
-    const uint16_t *wb = wt + (step & 1) * GW_WT + l32 * GW_KS + 8 * kh;
+    const uint16_t *wb = wt + (step % S::WB) * GW_WT + l32 * GW_KS + 8 * kh;
     const unsigned char *xs = gw_lds + (wave_x - lds0) + (uint32_t)(step % GW_DX) * S::XSTAGE + xrow0;
 #pragma unroll
     for (int k = 0; k < GW_NKK; ++k) {
@@ -518,35 +538,50 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
     issue_x(q);
     issue_w(q + 2, wq[q + 2], wi[q + 2]);
   }
-  // sb and W(0) are followed by S::VMCNT ops
-  if constexpr (RPT == 1)
+  // WA = 1: sb and W(0) are followed by S::VMCNT ops (W(1), x(0), W(2),
+  // x(1), W(3)); WA = 2: sb, W(0) and W(1) by x(0), W(2), x(1), W(3).
+  if constexpr (S::WA == 2) {
+    static_assert(RPT == 1, "two steps ahead: the 256-token tiles only");
+    asm volatile("s_waitcnt vmcnt(%5)"
+                 : "+v"(wq[0][0]), "+v"(wi[0][0]), "+v"(wq[1][0]), "+v"(wi[1][0]), "+v"(sbv[0])
+                 : "n"(S::VMCNT) : "memory");
+  } else if constexpr (RPT == 1) {
     asm volatile("s_waitcnt vmcnt(%3)" : "+v"(wq[0][0]), "+v"(wi[0][0]), "+v"(sbv[0])
                  : "n"(S::VMCNT) : "memory");
-  else
+  } else {
     asm volatile("s_waitcnt vmcnt(%6)"
                  : "+v"(wq[0][0]), "+v"(wi[0][0]), "+v"(wq[0][RPT - 1]), "+v"(wi[0][RPT - 1]),
                    "+v"(sbv[0]), "+v"(sbv[RPT - 1])
                  : "n"(S::VMCNT) : "memory");
+  }
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     d[j] = h2f((uint16_t)(sbv[j] & 0xFFFFu));
     dm[j] = h2f((uint16_t)(sbv[j] >> 16));
   }
   store_w(wq[0], wi[0], 0, 0);
+  if constexpr (S::WA == 2) store_w(wq[1], wi[1], 1, 1);
   __syncthreads();
 
   // One step: issue x(st + GW_DX - 1) and W(st + GW_DW) (into W(st)'s slot,
-  // stored a step ago), wait for x(st) and W(st + 1), multiply, dequantise
-  // W(st + 1).
+  // stored WA steps ago), wait for x(st) and W(st + WA), multiply, dequantise
+  // W(st + WA) into W buffer (st + WA) % WB. With WA = 1 a barrier after
+  // every step. With WA = 2 a barrier after every odd step: W(st + 2) is
+  // stored at step st and read at step st + 2, with a barrier after st or
+  // st + 1 between; its buffer held W(st - 2), read at step st - 2, with a
+  // barrier after st - 2 or st - 1 between. (One barrier a step with two
+  // buffers: batched 0.5B gate|up 141 us; none at all, results wrong, 112
+  // us.)
 #define GW_STEP(U)                                                              \
   {                                                                             \
     const int st = st0 + (U);                                                   \
     issue_x(st + GW_DX - 1);                                                    \
     issue_w(st + GW_DW, wq[(U) % GW_DW], wi[(U) % GW_DW]);                      \
-    GW_WAIT(((U) + 1) % GW_DW, S::VMCNT)                                        \
+    GW_WAIT(((U) + S::WA) % GW_DW, S::VMCNT)                                    \
     compute(st);                                                                \
-    store_w(wq[((U) + 1) % GW_DW], wi[((U) + 1) % GW_DW], st + 1, (st + 1) & 1); \
-    __syncthreads();                                                            \
+    store_w(wq[((U) + S::WA) % GW_DW], wi[((U) + S::WA) % GW_DW], st + S::WA,   \
+            (st + S::WA) % S::WB);                                              \
+    if (S::WA == 1 || ((U) & 1)) __syncthreads();                               \
   }
   // Whole rounds of GW_DW steps in a loop with no exit inside it, then the
   // remaining steps. (With a `break` after each step inside one loop, the
