@@ -981,15 +981,17 @@ __global__ __launch_bounds__(64 * RR_WAVES) void gemm_reduce_rope_kernel(
 
 namespace {
 // The tile family: the 128 x 128 wide tiles (32x32x16 MFMA) unless
-// WST_GEMM_TILES=narrow selects the 64 x 64 tiles (16x16x32 MFMA). One choice
-// for every chunk GEMM form, so fused and unfused forms sum alike.
-bool wide_tiles() {
+// WST_GEMM_TILES=narrow selects the 64 x 64 tiles (16x16x32 MFMA) and
+// WST_GEMM_TILES=wide the wide tiles wherever they apply (for measurement);
+// unset, the shape picks. One choice for every chunk GEMM form, so fused and
+// unfused forms sum alike.
+int gemm_tiles_mode() {  // 0 narrow, 1 by shape, 2 wide
   static int v = -1;
   if (v < 0) {
     const char *e = getenv("WST_GEMM_TILES");
-    v = (e && e[0] == 'n') ? 0 : 1;
+    v = (e && e[0] == 'n') ? 0 : (e && e[0] == 'w') ? 2 : 1;
   }
-  return v == 1;
+  return v;
 }
 
 template <bool HIER, bool SWI>
@@ -1038,9 +1040,14 @@ static int gemm_bn_override() {
 
 // Splits so that the grid covers the chip, each at least one step long.
 // rows: the weight matrix's row count (2 * inter for the SwiGLU form), which
-// with in_f picks the tiles: the wide tiles for long rows or many of them,
-// where their deeper pipeline pays; short K with few rows (the 0.5B qkv and
-// o projections) splits K into pieces too short for it.
+// with in_f and the plan's token count picks the tiles: the wide tiles for
+// long rows or many of them, where their deeper pipeline pays, and for any
+// shape whose 256-token tiles fill half the CUs without a split (the 0.5B
+// qkv and o projections over a 4096-token batched prefill: 30.3 -> 28.6 and
+// 25.0 -> 17.0 us, config 4 464-466k -> 475-480k tok/s); otherwise (the
+// same projections on one 256-token chunk: wide 9.0 + 3.9 us against narrow
+// 7.4 + 3.9 us for qkv) the narrow tiles, since short K split into pieces is
+// too short for the wide tiles' pipeline.
 // plan_n: the token count whose tiling and split-K plan the launch uses; n
 // may exceed it (several chunks in one launch): the grid then repeats the
 // plan's token tiles over n, and every token gets the bits a launch of
@@ -1052,7 +1059,10 @@ GemmPlan plan_gemm(int in_f, int out_f, int n, bool hier = true, int rows = 0, b
   if (rows <= 0) rows = out_f;
   const int pn = plan_n > 0 && plan_n < n ? plan_n : n;
   // (The wide tiles address x with 32-bit byte offsets.)
-  p.wide = hier && wide_tiles() && in_f >= GW_KC && (in_f >= 2048 || rows >= 4096) &&
+  const int tm = gemm_tiles_mode();
+  const int rows_t256 = ((rows + GW_BM - 1) / GW_BM) * ((pn + 255) / 256);
+  p.wide = hier && tm > 0 && in_f >= GW_KC &&
+           (tm == 2 || in_f >= 2048 || rows >= 4096 || rows_t256 >= wst_cu_count() / 2) &&
            (size_t)n * in_f * 2 < ((size_t)1 << 31);
   // Wide tiles of 128 tokens for the split-K shapes (256-token tiles fewer
   // than half the CUs), where 256-token tiles would leave CUs without a
