@@ -83,8 +83,16 @@ def test_gemm_norm_chunk_equals_gemm_then_rmsnorm(orc, wk, in_f, out_f, n, accum
 @pytest.mark.parametrize("in_f,n_q,n_kv,hd,pos0,n,qk", [(896, 14, 2, 64, 0, 256, False),
                                                         (896, 14, 2, 64, 300, 256, True),
                                                         (3584, 28, 4, 128, 5, 37, False),
-                                                        (512, 8, 2, 128, 60, 3, True)])
+                                                        (512, 8, 2, 128, 60, 3, True),
+                                                        (896, 14, 2, 64, 0, 2048, True),
+                                                        (896, 14, 2, 64, 100, 2000, False)])
 def test_gemm_rope_chunk_equals_gemm_then_rope_cache(orc, wk, in_f, n_q, n_kv, hd, pos0, n, qk):
+    """The fused qkv form against the GEMM then wst_rope_cache_chunk, bit for
+    bit (q rotated, k and v as computed, the cache rows). At head_dim 64 with
+    about 1800 tokens or more the GEMM runs unsplit on 256-token tiles, one
+    head a tile, and the tile's epilogue does the norm, rotation and append
+    (the last two cases, one with a ragged last tile); below that a reduce
+    kernel does them after the GEMM."""
     out_f = (n_q + 2 * n_kv) * hd
     max_seq = pos0 + n + 7
     lin = _lin(orc, wk, 41, in_f, out_f)

@@ -351,6 +351,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_mfma_kernel(
 //   0..31 of a tile are gate rows a0..a0+31 and rows 32..63 the up rows
 //   inter+a0.., and the epilogue writes act = f16(silu(gate) * up).
 #define GW_BM 64
+#define GW_ROPE_HD 64                   // head_dim of the RoPE epilogue: one tile's rows
 #define GW_KG 2
 #define GW_KC (GW_KG * HGROUP)          // 64 columns per step
 #define GW_KS (GW_KC + 8)               // W tile row stride in halves
@@ -394,11 +395,83 @@ struct GwShape {
 
 typedef float gm_f16v __attribute__((ext_vector_type(16)));
 
-template <bool HIER, bool SWI, int NWV>
+// The qkv GEMM's RoPE epilogue (ROPE tiles, head_dim 64 = one tile's rows):
+// what gemm_reduce_rope_kernel does after an unsplit GEMM, per token.
+struct GwRope {
+  uint16_t *k_cache, *v_cache;
+  const float *cos_tab, *sin_tab;
+  const uint16_t *q_norm_w, *k_norm_w;
+  int n_q, n_kv, pos0, max_seq;
+  float eps;
+};
+
+// RT tokens of one head of 64, stage by stage so that the tokens' dependent
+// chains (cross-lane swap, norm reduction, square root) overlap: lane j holds
+// column j of each (the value after the GEMM and bias); q is QK-normed,
+// rotated and stored to its row, k stored to its row as computed and rotated
+// into the cache, v stored to its row and the cache. The arithmetic is
+// gemm_reduce_rope_kernel's NARROW form (column j in lane j, the rotation
+// partner over a 32-lane swap, the norm's pair sums over the wave), so the
+// two give the same bits. ok[u]: token u exists (uniform in the wave).
+template <int RT>
+__device__ __forceinline__ void gw_rope_tokens(const float (&mine)[RT], const bool (&ok)[RT],
+                                               const int (&tok)[RT], int h, float *__restrict__ y,
+                                               int row_stride, const GwRope &re,
+                                               const float (&c)[RT], const float (&s)[RT],
+                                               float gq1, float gq2, int lane) {
+  const int hd = GW_ROPE_HD;
+  const bool hi = lane >= 32;
+  int pos[RT];
+#pragma unroll
+  for (int u = 0; u < RT; ++u) pos[u] = min(max(re.pos0 + tok[u], 0), re.max_seq - 1);
+  if (h >= re.n_q + re.n_kv) {  // v
+    const int kvh = h - re.n_q - re.n_kv;
+#pragma unroll
+    for (int u = 0; u < RT; ++u)
+      if (ok[u]) {
+        y[(size_t)tok[u] * row_stride + h * hd + lane] = mine[u];
+        re.v_cache[((size_t)kvh * re.max_seq + pos[u]) * hd + lane] = f2h(mine[u]);
+      }
+    return;
+  }
+  const bool is_q = h < re.n_q;
+  float x1[RT], x2[RT];
+#pragma unroll
+  for (int u = 0; u < RT; ++u) {
+    const float other = __shfl_xor(mine[u], 32);
+    x1[u] = hi ? other : mine[u];
+    x2[u] = hi ? mine[u] : other;
+  }
+  if (is_q ? re.q_norm_w : re.k_norm_w) {
+    float ss[RT];
+#pragma unroll
+    for (int u = 0; u < RT; ++u) ss[u] = wave_sum(!hi ? fmaf(x1[u], x1[u], x2[u] * x2[u]) : 0.0f);
+#pragma unroll
+    for (int u = 0; u < RT; ++u) {
+      const float sc = 1.0f / sqrtf(ss[u] / (float)hd + re.eps);
+      x1[u] = x1[u] * sc * gq1;
+      x2[u] = x2[u] * sc * gq2;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < RT; ++u) {
+    if (!ok[u]) continue;
+    const float lo = rope_lo(x1[u], x2[u], c[u], s[u]), hv = rope_hi(x1[u], x2[u], c[u], s[u]);
+    float *row = y + (size_t)tok[u] * row_stride;
+    if (is_q) {
+      row[h * hd + lane] = hi ? hv : lo;
+    } else {
+      row[h * hd + lane] = mine[u];  // k as computed
+      re.k_cache[((size_t)(h - re.n_q) * re.max_seq + pos[u]) * hd + lane] = f2h(hi ? hv : lo);
+    }
+  }
+}
+
+template <bool HIER, bool SWI, int NWV, bool ROPE = false>
 __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
     const void *__restrict__ w, const uint8_t *__restrict__ si, const uint32_t *__restrict__ sb,
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ bias, float *__restrict__ y,
-    float *__restrict__ ws, int in_f, int out_f, int n, int accum, int gps) {
+    float *__restrict__ ws, int in_f, int out_f, int n, int accum, int gps, GwRope re) {
 #pragma clang fp contract(off)
   static_assert(HIER, "the wide tiles take int4-hier weights");
   using S = GwShape<NWV>;
@@ -619,6 +692,20 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
                  :: "memory");
   __syncthreads();
 
+  // RoPE epilogue: the rotation angles of the wave's tokens (every NWV-th of
+  // the tile's), loaded while the accumulators go through LDS.
+  constexpr int RTOK = ROPE ? BN / NWV : 1;
+  float rc[RTOK], rsn[RTOK];
+  if constexpr (ROPE) {
+    const int half = GW_ROPE_HD / 2, jj = lane & 31;
+#pragma unroll
+    for (int i = 0; i < RTOK; ++i) {
+      const int pos = min(max(re.pos0 + t0 + wave + i * NWV, 0), re.max_seq - 1);
+      rc[i] = re.cos_tab[(size_t)pos * half + jj];
+      rsn[i] = re.sin_tab[(size_t)pos * half + jj];
+    }
+  }
+
   // Epilogue through LDS, token-major: accumulator r of row tile a holds row
   // 32 a + 8 (r / 4) + 4 (lane / 32) + r % 4, token lane % 32 of the wave.
   float *ct = (float *)gw_lds;  // [BN][GW_CS]
@@ -630,6 +717,34 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(
       ct[(wave * 32 + l32) * GW_CS + row] = acc[a][r];
     }
   __syncthreads();
+  if constexpr (ROPE) {
+    // the tile's 64 rows are head h; each wave takes every NWV-th token
+    static_assert(!SWI && GW_BM == GW_ROPE_HD, "the RoPE tiles are one head of the plain GEMM");
+    const int h = r0 / GW_BM, half = GW_ROPE_HD / 2, jj = lane & 31;
+    const float bj = bias ? h2f(bias[r0 + lane]) : 0.0f;
+    const uint16_t *g = h < re.n_q ? re.q_norm_w : re.k_norm_w;
+    const float gq1 = g ? h2f(g[jj]) : 0.0f, gq2 = g ? h2f(g[jj + half]) : 0.0f;
+    constexpr int RT = 4;
+    static_assert(RTOK % RT == 0, "tokens in groups of four");
+#pragma unroll
+    for (int i0 = 0; i0 < RTOK; i0 += RT) {
+      float mine[RT], c[RT], sn[RT];
+      bool ok[RT];
+      int tok[RT];
+#pragma unroll
+      for (int u = 0; u < RT; ++u) {
+        const int tl = wave + (i0 + u) * NWV;
+        tok[u] = t0 + tl;
+        ok[u] = tok[u] < n;
+        mine[u] = ct[tl * GW_CS + lane];
+        if (bias) mine[u] += bj;
+        c[u] = rc[i0 + u];
+        sn[u] = rsn[i0 + u];
+      }
+      gw_rope_tokens<RT>(mine, ok, tok, h, y, out_f, re, c, sn, gq1, gq2, lane);
+    }
+    return;
+  }
   if constexpr (SWI) {
     uint16_t *act = (uint16_t *)y;
     const int a0 = r0 / 2;
@@ -1110,11 +1225,11 @@ void launch_gemm(const GemmPlan &p, const void *w, const void *si, const void *s
       if (p.nwv == 4)
         gemm_wide_kernel<HIER, SWI, 4><<<p.grid, GwShape<4>::THREADS, GwShape<4>::LDS, WST_STREAM>>>(
             w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
-            (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps);
+            (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps, GwRope{});
       else
         gemm_wide_kernel<HIER, SWI, 8><<<p.grid, GwShape<8>::THREADS, GwShape<8>::LDS, WST_STREAM>>>(
             w, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
-            (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps);
+            (const uint16_t *)bias, (float *)y, ws, in_f, out_f, n, accum, p.gps, GwRope{});
       return;
     }
   }
@@ -1262,6 +1377,17 @@ extern "C" wst_status_t wst_gemm_hier_norm_chunk(const void *qw, const void *si,
                                    h_out, n);
 }
 
+// WST_GEMM_ROPE_EPI=0 keeps the separate reduce + RoPE kernel on the shapes
+// the GEMM's own RoPE epilogue covers (for measurement and the parity test).
+static bool rope_epilogue_on() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("WST_GEMM_ROPE_EPI");
+    v = (e && e[0] == '0') ? 0 : 1;
+  }
+  return v == 1;
+}
+
 extern "C" wst_status_t wst_gemm_hier_rope_chunks(const void *qw, const void *si, const void *sb,
                                                  const void *x, const void *bias, void *qkv,
                                                  int32_t in_f, void *k_cache, void *v_cache,
@@ -1280,6 +1406,30 @@ extern "C" wst_status_t wst_gemm_hier_rope_chunks(const void *qw, const void *si
               "wst_gemm_hier_rope_chunk: null pointer");
   WST_REQUIRE(max_seq > 0 && pos0 >= 0 && pos0 + n <= max_seq,
               "wst_gemm_hier_rope_chunk: chunk does not fit the cache");
+  // head_dim 64 on unsplit 256-token wide tiles (a batched prefill of the
+  // 0.5B shape): each tile is one head, and its epilogue applies the norm,
+  // the rotation and the cache append itself, in the reduce kernel's
+  // arithmetic; no partials, no second launch.
+  {
+    const GemmPlan p = plan_gemm(in_f, out_f, n, true, 0, false, plan_n);
+    if (p.wide && p.nwv == 8 && p.splits == 1 && head_dim == GW_ROPE_HD && rope_epilogue_on()) {
+      static bool attr = false;
+      if (!attr) {
+        (void)hipFuncSetAttribute((const void *)gemm_wide_kernel<true, false, 8, true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, GwShape<8>::LDS);
+        attr = true;
+      }
+      const GwRope re{(uint16_t *)k_cache, (uint16_t *)v_cache, (const float *)cos_tab,
+                      (const float *)sin_tab, (const uint16_t *)q_norm_w,
+                      (const uint16_t *)k_norm_w, n_q, n_kv, pos0, max_seq, eps};
+      gemm_wide_kernel<true, false, 8, true><<<p.grid, GwShape<8>::THREADS, GwShape<8>::LDS,
+                                               WST_STREAM>>>(
+          qw, (const uint8_t *)si, (const uint32_t *)sb, (const uint16_t *)x,
+          (const uint16_t *)bias, (float *)qkv, nullptr, in_f, out_f, n, 0, p.gps, re);
+      WST_TRY_KERNEL("wst_gemm_hier_rope_chunk");
+      return WST_OK;
+    }
+  }
   float *ws;
   int splits;
   st = gemm_to_scratch(qw, si, sb, x, in_f, out_f, n, &ws, &splits, plan_n);
