@@ -80,24 +80,29 @@ def test_gemm_norm_chunk_equals_gemm_then_rmsnorm(orc, wk, in_f, out_f, n, accum
     assert np.array_equal(ha.numpy().view(np.uint16), hb.numpy().view(np.uint16))
 
 
-@pytest.mark.parametrize("in_f,n_q,n_kv,hd,pos0,n,qk", [(896, 14, 2, 64, 0, 256, False),
-                                                        (896, 14, 2, 64, 300, 256, True),
-                                                        (3584, 28, 4, 128, 5, 37, False),
-                                                        (512, 8, 2, 128, 60, 3, True),
-                                                        (896, 14, 2, 64, 0, 2048, True),
-                                                        (896, 14, 2, 64, 100, 2000, False)])
-def test_gemm_rope_chunk_equals_gemm_then_rope_cache(orc, wk, in_f, n_q, n_kv, hd, pos0, n, qk):
+@pytest.mark.parametrize("in_f,n_q,n_kv,hd,pos0,n,qk,has_bias",
+                         [(896, 14, 2, 64, 0, 256, False, True),
+                          (896, 14, 2, 64, 300, 256, True, True),
+                          (3584, 28, 4, 128, 5, 37, False, True),
+                          (512, 8, 2, 128, 60, 3, True, True),
+                          (896, 14, 2, 64, 0, 2048, True, True),
+                          (896, 14, 2, 64, 100, 2000, False, True),
+                          (896, 14, 2, 64, 6, 2050, True, False)])
+def test_gemm_rope_chunk_equals_gemm_then_rope_cache(orc, wk, in_f, n_q, n_kv, hd, pos0, n, qk,
+                                                     has_bias):
     """The fused qkv form against the GEMM then wst_rope_cache_chunk, bit for
     bit (q rotated, k and v as computed, the cache rows). At head_dim 64 with
     about 1800 tokens or more the GEMM runs unsplit on 256-token tiles, one
     head a tile, and the tile's epilogue does the norm, rotation and append
-    (the last two cases, one with a ragged last tile); below that a reduce
-    kernel does them after the GEMM."""
+    (the last three cases: one with a ragged last tile, one without a bias,
+    as Qwen3's projections have none, ending at the cache's last row); below
+    that a reduce kernel does them after the GEMM."""
     out_f = (n_q + 2 * n_kv) * hd
-    max_seq = pos0 + n + 7
+    max_seq = pos0 + n + (7 if has_bias else 0)
     lin = _lin(orc, wk, 41, in_f, out_f)
     x = _x(orc, wk, 42, n, in_f)
-    b = dev_f16(wk, f16(orc, orc.fixture_normal(41, 3, out_f, 0.3)))
+    b = dev_f16(wk, f16(orc, orc.fixture_normal(41, 3, out_f, 0.3))) if has_bias else None
+    bp = b.ptr if has_bias else None
     qn = dev_f16(wk, f16(orc, 1.0 + orc.fixture_normal(41, 4, hd, 0.1))) if qk else None
     kn = dev_f16(wk, f16(orc, 1.0 + orc.fixture_normal(41, 5, hd, 0.1))) if qk else None
     c, s = orc.rope_table(max_seq, hd, 1e6)
@@ -108,11 +113,11 @@ def test_gemm_rope_chunk_equals_gemm_then_rope_cache(orc, wk, in_f, n_q, n_kv, h
         bufs.append((wk.DeviceBuffer(n * out_f, np.float32), dev_f16(wk, kv0), dev_f16(wk, kv0)))
     qp, kp = (qn.ptr if qk else None), (kn.ptr if qk else None)
     (qa, ka, va), (qb, kb, vb) = bufs
-    ffi.call("wst_gemm_int4_hier", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, x.ptr, b.ptr, qa.ptr, in_f,
+    ffi.call("wst_gemm_int4_hier", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, x.ptr, bp, qa.ptr, in_f,
              out_f, n, 0)
     ffi.call("wst_rope_cache_chunk", qa.ptr, ka.ptr, va.ptr, cd.ptr, sd.ptr, n_q, n_kv, hd, pos0,
              n, max_seq, qp, kp, 1e-6)
-    ffi.call("wst_gemm_hier_rope_chunk", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, x.ptr, b.ptr,
+    ffi.call("wst_gemm_hier_rope_chunk", lin.qw.ptr, lin.si.ptr, lin.sb.ptr, x.ptr, bp,
              qb.ptr, in_f, kb.ptr, vb.ptr, cd.ptr, sd.ptr, n_q, n_kv, hd, pos0, n, max_seq, qp,
              kp, 1e-6)
     assert np.array_equal(qa.numpy().view(np.uint32), qb.numpy().view(np.uint32))
