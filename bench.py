@@ -247,6 +247,15 @@ def cpu_leg(g, cfg, ctx0, first_token, gpu_tokens, gpu_logits0, budget_s, same_c
         tb.pos = ctx0
         _, lg_text = tb.step(first_token)
         tb.close()
+        # the same step in the reference CUDA kernels' own arithmetic (f16
+        # group sums, their reduction orders): how far the reference itself
+        # lands from the precision-mirrored f64 forward
+        rf = O.State(o, ctx0 + 64, 0)
+        rf.fill_kv(KV_SEED, ctx0)
+        rf.pos = ctx0
+        with O.variant(O.ACC_REF):
+            _, lg_ref = rf.step(first_token)
+        rf.close()
     st.close()
     n = len(toks)
     # The reference's CPU path dequantises the model once (whetstone-quant)
@@ -285,6 +294,9 @@ def cpu_leg(g, cfg, ctx0, first_token, gpu_tokens, gpu_logits0, budget_s, same_c
         "first_step_logits_max_abs": float(diff.max()),
         "first_step_logits_max_rel": float(rel.max()),
         "first_step_within_tolerance": bool(np.allclose(gpu_logits0, lg0, rtol=1e-3, atol=1e-2)),
+        "first_step_reference_arithmetic_max_abs": float(np.max(np.abs(lg_ref - lg0))),
+        "first_step_gpu_at_most_reference_distance": bool(
+            diff.max() <= np.max(np.abs(lg_ref.astype(np.float64) - lg0))),
         "first_step_top2_margin": O.top2_margin(lg0),
         "first_step_gpu_vs_textbook_max_abs": float(np.max(np.abs(gpu_logits0 - lg_text))),
         "first_step_mirrored_vs_textbook_max_abs": float(np.max(np.abs(lg0 - lg_text))),
