@@ -760,7 +760,12 @@ struct HierArgs {
 // Units in flight per row slot. Measured on the 7B shapes: a second buffer
 // helps only when a slot streams many units (the head, ~37 per slot); for the
 // block GEMVs (1 to 5 units per slot) the extra up-front loads cost more than
-// they hide. WST_GEMV_PD=1 or 2 forces one choice.
+// they hide (7B step 790 -> 738 tok/s with two everywhere). Rows that share a
+// wave (in_f <= 1024, four rows of 16 lanes) take two regardless: their
+// loads per unit are small, and on the 0.5B block GEMVs two units in flight
+// measured faster (norm + qkv 4.09 -> 3.39 us; config-2 step 1,745-1,748 ->
+// 1,825-1,830 tok/s, three and four units 1,754 and 1,686). A row's bits do
+// not depend on this. WST_GEMV_PD=1..4 forces one choice.
 static int gemv_pd_override() {
   static int v = -1;
   if (v < 0) {
@@ -816,7 +821,7 @@ static int launch_q(const HierArgs &a) {
     int pd = gemv_pd_override();
     if (pd < 1 || pd > 4) {
       const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR * RPW);
-      pd = a.nunits >= 8 * slots ? 2 : 1;
+      pd = a.nunits >= 8 * slots || RPW > 1 ? 2 : 1;
     }
     if (pd == 1) return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX, XT, TW>(a);
     if (pd == 3) return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM, AX, XT, TW>(a);
