@@ -490,7 +490,15 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       const float dm = h2f((uint16_t)(B.sbv[k] >> 16));
       lv[k] = d * as[k] - dm * am[k];
     }
-    load_unit(B, row0(it + PD) + rs);
+    // The next unit's loads. With one unit in flight they are skipped when
+    // that unit lies past the last row (a wave-uniform branch): issued
+    // anyway, clamped to the last row, every wave of the grid ended on a
+    // request to the same few cache lines (7B step 788 -> 797-804 tok/s,
+    // 0.5B 1,806 -> 1,878-1,901). The next compute waits for this unit's
+    // loads in any case. With two or more in flight the branch made the
+    // compiler wait for every outstanding load (7B head 48.3 -> 54.1 us), so
+    // those keep the clamped loads.
+    if (PD > 1 || row0(it + PD) + rs < nunits) load_unit(B, row0(it + PD) + rs);
     float part[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) part[k] = WPR > 1 ? wave_sum(lv[k]) : slot_sum<LPR>(lv[k]);
@@ -760,11 +768,7 @@ struct HierArgs {
 // Units in flight per row slot. Measured on the 7B shapes: a second buffer
 // helps only when a slot streams many units (the head, ~37 per slot); for the
 // block GEMVs (1 to 5 units per slot) the extra up-front loads cost more than
-// they hide (7B step 790 -> 738 tok/s with two everywhere). Rows that share a
-// wave (in_f <= 1024, four rows of 16 lanes) take two regardless: their
-// loads per unit are small, and on the 0.5B block GEMVs two units in flight
-// measured faster (norm + qkv 4.09 -> 3.39 us; config-2 step 1,745-1,748 ->
-// 1,825-1,830 tok/s, three and four units 1,754 and 1,686). A row's bits do
+// they hide (7B step 790 -> 738 tok/s with two everywhere). A row's bits do
 // not depend on this. WST_GEMV_PD=1..4 forces one choice.
 static int gemv_pd_override() {
   static int v = -1;
@@ -821,7 +825,7 @@ static int launch_q(const HierArgs &a) {
     int pd = gemv_pd_override();
     if (pd < 1 || pd > 4) {
       const int slots = wst_cu_count() * blocks_per_cu() * (NT / 64 / WPR * RPW);
-      pd = a.nunits >= 8 * slots || RPW > 1 ? 2 : 1;
+      pd = a.nunits >= 8 * slots ? 2 : 1;
     }
     if (pd == 1) return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 1, RPW, AM, AX, XT, TW>(a);
     if (pd == 3) return launch_pd<NG, WPR, XB, NT, NORM, SWIGLU, 3, RPW, AM, AX, XT, TW>(a);
