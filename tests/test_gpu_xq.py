@@ -65,7 +65,11 @@ def test_table_decodes_to_the_oracle_xq14(orc, wk):
 
 @pytest.mark.parametrize("in_f,out_f,bias,accum", [(18944, 3584, False, 1), (3584, 3584, False, 1),
                                                    (4864, 896, False, 1), (896, 1152, True, 0),
-                                                   (3584, 600, True, 1)])
+                                                   (3584, 600, True, 1),
+                                                   # head shapes: two units in flight, the
+                                                   # second issued after the table's DMA
+                                                   (896, 151936, False, 0),
+                                                   (3584, 152064, False, 0)])
 def test_gemv_on_a_table_equals_gemv_on_x(orc, wk, in_f, out_f, bias, accum):
     qw = wk.DeviceBuffer(out_f * in_f // 8, np.uint32)
     si = wk.DeviceBuffer(out_f * in_f // 32, np.uint8)

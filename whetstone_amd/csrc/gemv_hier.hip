@@ -350,8 +350,10 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
       }
     }
   };
-#pragma unroll
-  for (int i = 0; i < PD; ++i) load_unit(bufs[i], row0(i) + rs);
+  // (units 1..PD-1 go out after the table: issued here they would queue the
+  // activation fetch behind them; 0.5B head 5.06 -> 5.21 TB/s over six A/B
+  // pairs)
+  load_unit(bufs[0], row0(0) + rs);
 
   // 3. the RMS scale (rms_scale512's order: thread t, blocks t, t+512, ...)
   float s = 1.0f;
@@ -370,11 +372,12 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
 
   // 4. the table
   if constexpr (XT) {
-    // The DMA went out before the first units' loads (2 per group and row:
-    // packed bytes and scale index); waiting for all but those many leaves
-    // the weights in flight. (Where the compiler loads the row scales with
-    // vector loads too, the wait also covers the first of the weights.)
-    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * NR * NG * PD) : "memory");
+    // The DMA went out before the first unit's loads (2 per group and row:
+    // packed bytes and scale index; later units go out after the table);
+    // waiting for all but those many leaves the weights in flight. (Where the
+    // compiler loads the row scales with vector loads too, the wait also
+    // covers the first of the weights.)
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * NR * NG) : "memory");
   }
 #pragma unroll
   for (int i = 0; i < (XT ? 0 : XB); ++i) {
@@ -402,6 +405,8 @@ __global__ __launch_bounds__(NT) void gemv_hier_kernel(
     build_xq(h, b, b < NB8, xgt);
   }
   __syncthreads();
+#pragma unroll
+  for (int i = 1; i < PD; ++i) load_unit(bufs[i], row0(i) + rs);
 
   // A lane's groups are the same for every unit, so with at most two groups
   // per lane their table entries move to registers once, here, instead of
